@@ -1,0 +1,159 @@
+"""Packed causal attention throughput on one MI355X.
+
+A step is one forward pass of the packed attention over one synthetic pack. The default workload is the
+Gemma-31B-class global layer at 32,768 tokens (one causal segment, 32 query / 16 KV heads, head_dim 128, bf16): the
+configuration the metric is quoted on. Inputs are resident in HBM before the timed region; the pack's work list is
+built once (as the reference plans a pack once for all layers), so each timed step launches the attention kernel
+alone, on the current stream, timed with HIP events.
+
+Prints one JSON line: value = TFLOP/s counting only unmasked (query, key) pairs (4 * D * H per pair), with the
+roofline of the attention kernel (dense bf16 MFMA peak) and the CPU baseline (the reference's torch SDPA path,
+restated in oracle/attention.py, timed on this host's cores on a bounded sample of the same workload).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+METRIC = "packed causal attention TFLOP/s + % bf16 MFMA peak @32k tokens, 1 GPU"
+#: MI355X dense bf16 MFMA peak: 256 CUs x 2.4 GHz x 4096 FLOP/clk/CU (AMD's published 2.5 PFLOP/s).
+PEAK_BF16_TFLOPS = 2516.6
+PEAK_HBM_GBS = 8000.0
+TRAFFIC = ROOT / "profiles" / "traffic.json"
+
+
+def parse() -> argparse.Namespace:
+    p = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--workload", default="global32k",
+                   help="global32k (default), global131k, qwen, sliding, multimodal, tiny")
+    p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-repeats", type=int, default=3)
+    return p.parse_args()
+
+
+def cpu_baseline(w, repeats: int) -> dict:
+    """The oracle (the reference's per-sequence torch SDPA path) on the host cores, on one KV-head group of the pack
+    (its query heads over every sequence), median of ``repeats`` runs after one warm-up, for bf16 and fp32 inputs;
+    the faster is reported. TFLOP/s counts the same unmasked pairs as the GPU figure."""
+    import torch
+
+    from oracle import attention as oracle_attention
+
+    torch.set_num_threads(int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)))
+    group = w.heads // w.kv_heads
+    q = w.query[:, :group].cpu()
+    k = w.key[:, :1].cpu()
+    v = w.value[:, :1].cpu()
+    sample_flops = w.flops() * group / w.heads
+    best = None
+    times_by_dtype = {}
+    for dtype in (torch.bfloat16, torch.float32):
+        times = []
+        for n in range(repeats + 1):
+            t0 = time.perf_counter()
+            oracle_attention.packed_attention(q, k, v, w.q_cu, w.k_cu, w.scale, w.window_left, w.window_right,
+                                              w.spans, dtype=dtype)
+            if n:
+                times.append(time.perf_counter() - t0)
+        med = statistics.median(times)
+        times_by_dtype[str(dtype).split(".")[-1]] = med
+        if best is None or med < best[1]:
+            best = (dtype, med)
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    dtype, sec = best
+    return {
+        "value": round(sample_flops / sec / 1e12, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"{w.name}: query heads 0-{group - 1} (KV head 0) of {w.heads}, all {w.tokens} tokens; "
+                   f"torch {torch.__version__} CPU SDPA per sequence; median of {repeats} after 1 warm-up; "
+                   f"seconds bf16 {times_by_dtype['bfloat16']:.3f}, fp32 {times_by_dtype['float32']:.3f}; "
+                   f"reported {str(dtype).split('.')[-1]}; os.cpu_count()={os.cpu_count()}; {cpu_model}"),
+    }
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": f"--gpus {args.gpus}: this build measures one GPU only; the attention kernel "
+                                   "runs on one GPU's share (see DESIGN.md for how it would shard)"}))
+        return 2
+    import torch
+
+    from karpo_decision_amd import ops, workloads
+
+    device = torch.device("cuda", 0)
+    w = workloads.named(args.workload, device, args.seed)
+    q_cu = torch.tensor(w.q_cu, dtype=torch.int32, device=device)
+    k_cu = torch.tensor(w.k_cu, dtype=torch.int32, device=device)
+    spans = torch.tensor(w.spans, dtype=torch.int32, device=device) if w.spans else None
+    plan = ops.make_plan(w.q_cu, w.k_cu, w.heads, w.kv_heads, w.head_dim, w.window_left, w.window_right, device)
+
+    def step():
+        return ops.run(w.query, w.key, w.value, q_cu, k_cu, w.max_q, w.scale, w.window_left, w.window_right, spans,
+                       plan)
+
+    with torch.inference_mode():
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream(device)
+        marks = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                 for _ in range(args.steps)]
+        begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        begin.record(stream)
+        for a, b in marks:
+            a.record(stream)
+            step()
+            b.record(stream)
+        end.record(stream)
+        torch.cuda.synchronize()
+    total_ms = begin.elapsed_time(end)
+    launch_ms = statistics.mean(a.elapsed_time(b) for a, b in marks)
+    ms_per_step = total_ms / args.steps
+    flops = w.flops()
+    value = flops / (ms_per_step * 1e-3) / 1e12
+    achieved = flops / (launch_ms * 1e-3) / 1e12
+
+    traffic = None
+    if TRAFFIC.exists():
+        entry = json.loads(TRAFFIC.read_text()).get(w.name)
+        if entry:
+            traffic = entry.get("bytes_per_launch")
+    result = {
+        "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {**w.describe(), "pct_of_bf16_peak": round(100 * value / PEAK_BF16_TFLOPS, 2),
+                   "tokens_per_s": round(w.tokens / (ms_per_step * 1e-3)), "flops_per_step": flops,
+                   "min_hbm_bytes_per_step": w.bytes(), "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
+                     "kernel": f"attn_fwd_kernel<{w.head_dim}>", "avg_launch_ms": round(launch_ms, 4)},
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(w, args.cpu_repeats)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,112 @@
+/*
+ * karpo_attn.h - C ABI of the MI355X (gfx950) packed varlen attention forward.
+ *
+ * One call computes softmax(scale * Q K^T + mask) V for every virtual sequence of a padding-free pack:
+ * query rows q_cu[i]..q_cu[i+1] attend to key rows k_cu[i]..k_cu[i+1] of the same sequence, with the bottom-right
+ * alignment of varlen flash attention (query i sits at key coordinate i + Lk - Lq), an optional (left, right)
+ * window, GQA (query head h reads key/value head h / (heads / kv_heads)) and bidirectional spans (image blocks) that
+ * OR-in "same span" visibility on top of the window rule.
+ *
+ * Reference interfaces this ABI replaces (paths relative to the karpo-decision repository):
+ *   - src/karpo_decision/families/gemma/triton_attention.py:92-110   attend(query, key, value, q_cu, k_cu, max_q, scale)
+ *   - src/karpo_decision/families/gemma/sliding_attention.py:85-93   attend(..., max_q, max_k, scale, window)
+ *   - src/karpo_decision/families/qwen/packed.py:36-44, 119-125      varlen_attn(q, k, v, cu_q, cu_k, ..., window_size)
+ *   - src/karpo_decision/families/gemma/global_attention.py:71-79    padded(query, key, value, cu, size, causal, scale)
+ *   - src/karpo_decision/families/gemma/vision.py:198-210            see_whole(...) (image spans, folded into the mask)
+ *   - src/karpo_decision/families/gemma/packed.py:103-151            block_plan (the per-pack plan; karpo_attn_plan)
+ *
+ * Conventions: every pointer argument marked "device" is HIP device memory; sizes and strides are in elements;
+ * bf16 is passed as raw 16-bit storage. No entry point allocates, synchronises or copies between host and device;
+ * karpo_attn_fwd launches only on the given stream, reads q_cu/k_cu from device memory when its kernels run (so a
+ * captured graph may rewrite them between replays), and never aborts: failures are returned as a status code.
+ */
+#ifndef KARPO_ATTN_H
+#define KARPO_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+enum {
+  KARPO_ATTN_OK = 0,
+  KARPO_ATTN_ERR_NULL = 1,        /* a required pointer is NULL */
+  KARPO_ATTN_ERR_HEAD_DIM = 2,    /* head_dim not in {64, 128, 256} */
+  KARPO_ATTN_ERR_HEADS = 3,       /* heads or kv_heads < 1, or heads % kv_heads != 0 */
+  KARPO_ATTN_ERR_LAYOUT = 4,      /* head_dim not contiguous, a stride not a multiple of 8, or a base not 16-B aligned */
+  KARPO_ATTN_ERR_WORKSPACE = 5,   /* workspace NULL or smaller than karpo_attn_workspace_bytes */
+  KARPO_ATTN_ERR_WINDOW = 6,      /* a window side below -1 */
+  KARPO_ATTN_ERR_SPANS = 7,       /* n_spans < 0, or spans NULL with n_spans > 0 */
+  KARPO_ATTN_ERR_LAUNCH = 8,      /* the HIP runtime refused a launch */
+  KARPO_ATTN_ERR_ARG = 9,         /* a negative size or sequence count */
+  KARPO_ATTN_ERR_CAPACITY = 10,   /* karpo_attn_plan: the output buffer is too small */
+  KARPO_ATTN_ERR_BOUNDS = 11      /* karpo_attn_plan: host bounds not non-decreasing from 0 */
+};
+
+/* Everything one forward call needs. Tensors are bf16 with head_dim contiguous:
+ *   q[total_q, heads, head_dim], k/v[total_k, kv_heads, head_dim], o[total_q, heads, head_dim]
+ * addressed as base + row * stride_tok + head * stride_head + d. */
+typedef struct KarpoAttnArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  int64_t q_stride_tok, q_stride_head;
+  int64_t k_stride_tok, k_stride_head;
+  int64_t v_stride_tok, v_stride_head;
+  int64_t o_stride_tok, o_stride_head;
+  const int32_t* q_cu;   /* device, n_seq + 1 query row bounds */
+  const int32_t* k_cu;   /* device, n_seq + 1 key row bounds */
+  int32_t n_seq;
+  int32_t heads;
+  int32_t kv_heads;
+  int32_t head_dim;
+  int64_t total_q;       /* rows of q (sizes the launch) */
+  int32_t max_q;         /* an upper bound of every q_cu[i+1] - q_cu[i] (sizes the launch) */
+  float scale;           /* logits are scale * q.k */
+  int32_t window_left;   /* keys before the aligned query position a query sees; -1 unbounded */
+  int32_t window_right;  /* keys after it; -1 unbounded, 0 causal */
+  const int32_t* spans;  /* device, [n_spans][2] half-open query-row ranges [s, e) in pack rows, or NULL */
+  int32_t n_spans;       /* spans sorted by start, non-overlapping, each inside one sequence */
+  const int32_t* plan;   /* device plan from karpo_attn_plan (copied to the device), or NULL: plan on the device */
+  void* workspace;       /* device scratch of karpo_attn_workspace_bytes bytes (unused when plan != NULL) */
+  size_t workspace_bytes;
+} KarpoAttnArgs;
+
+/* Bytes of device workspace karpo_attn_fwd needs for these arguments when args->plan is NULL
+ * (reads only sizes: heads, kv_heads, head_dim, n_seq, total_q, max_q). */
+int karpo_attn_workspace_bytes(const KarpoAttnArgs* args, size_t* bytes);
+
+/* Int32 entries a plan buffer for these arguments holds at most (the capacity to give karpo_attn_plan). */
+int karpo_attn_plan_capacity(const KarpoAttnArgs* args, int64_t* entries);
+
+/* The forward pass on `stream` (a hipStream_t; NULL is the null stream). Plans on the device first unless
+ * args->plan is set. Replaces triton_attention.attend's launch (triton_attention.py:103-109); the caller owns o. */
+int karpo_attn_fwd(const KarpoAttnArgs* args, void* stream);
+
+/* The work list on the host from host copies of the bounds, in the layout the kernel reads:
+ *   plan[0] = tiles, plan[1] = query rows per tile, plan[2] = keys per step, plan[3] = heads per work item,
+ *   then per tile (segment, tile index), longest first (ties in segment, tile order).
+ * Replaces the host-side bound building of block_plan (families/gemma/packed.py:103-151); like it, it runs once per
+ * pack and its result is reused by every layer of the same geometry. Reads heads, kv_heads, head_dim, window_*. */
+int karpo_attn_plan(const KarpoAttnArgs* args, const int32_t* q_cu_host, const int32_t* k_cu_host, int32_t n_seq,
+                    int32_t* plan, int64_t capacity);
+
+/* Query rows per tile and keys per step the kernel uses for these heads / head size. */
+int karpo_attn_tile_shape(int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t* rows_per_tile,
+                          int32_t* keys_per_step, int32_t* heads_per_item);
+
+/* A static message for a status code. */
+const char* karpo_attn_strerror(int status);
+
+/* Library version, for loaders that check what they bound. */
+int karpo_attn_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KARPO_ATTN_H */

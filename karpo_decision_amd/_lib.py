@@ -1,0 +1,91 @@
+"""ctypes binding of ``libkarpo_attn.so`` (``include/karpo_attn.h``). The library is the only compute path: if it is
+missing this module raises, it never falls back to another implementation."""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+LIBRARY = Path(__file__).resolve().parent / "libkarpo_attn.so"
+
+#: Every symbol ``include/karpo_attn.h`` declares.
+EXPORTS = ("karpo_attn_fwd", "karpo_attn_plan", "karpo_attn_plan_capacity", "karpo_attn_workspace_bytes",
+           "karpo_attn_tile_shape", "karpo_attn_strerror", "karpo_attn_version")
+
+OK = 0
+ERR_HEAD_DIM, ERR_HEADS, ERR_LAYOUT, ERR_WINDOW, ERR_SPANS, ERR_ARG, ERR_BOUNDS = 2, 3, 4, 6, 7, 9, 11
+#: Status codes that mean "these arguments are not supported" (ValueError), the rest are runtime failures.
+VALUE_ERRORS = {1, ERR_HEAD_DIM, ERR_HEADS, ERR_LAYOUT, 5, ERR_WINDOW, ERR_SPANS, ERR_ARG, 10, ERR_BOUNDS}
+
+
+class KarpoAttnArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p), ("o", ctypes.c_void_p),
+        ("q_stride_tok", ctypes.c_int64), ("q_stride_head", ctypes.c_int64),
+        ("k_stride_tok", ctypes.c_int64), ("k_stride_head", ctypes.c_int64),
+        ("v_stride_tok", ctypes.c_int64), ("v_stride_head", ctypes.c_int64),
+        ("o_stride_tok", ctypes.c_int64), ("o_stride_head", ctypes.c_int64),
+        ("q_cu", ctypes.c_void_p), ("k_cu", ctypes.c_void_p),
+        ("n_seq", ctypes.c_int32), ("heads", ctypes.c_int32), ("kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("total_q", ctypes.c_int64), ("max_q", ctypes.c_int32), ("scale", ctypes.c_float),
+        ("window_left", ctypes.c_int32), ("window_right", ctypes.c_int32),
+        ("spans", ctypes.c_void_p), ("n_spans", ctypes.c_int32),
+        ("plan", ctypes.c_void_p), ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def load() -> ctypes.CDLL:
+    """The loaded library (loaded once). RuntimeError when it has not been built."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIBRARY.exists():
+            raise RuntimeError(f"{LIBRARY} is missing: build it first (python -m karpo_decision_amd.build); there "
+                               "is no fallback implementation")
+        lib = ctypes.CDLL(str(LIBRARY))
+        P = ctypes.POINTER
+        lib.karpo_attn_fwd.argtypes = [P(KarpoAttnArgs), ctypes.c_void_p]
+        lib.karpo_attn_fwd.restype = ctypes.c_int
+        lib.karpo_attn_plan.argtypes = [P(KarpoAttnArgs), P(ctypes.c_int32), P(ctypes.c_int32), ctypes.c_int32,
+                                        P(ctypes.c_int32), ctypes.c_int64]
+        lib.karpo_attn_plan.restype = ctypes.c_int
+        lib.karpo_attn_plan_capacity.argtypes = [P(KarpoAttnArgs), P(ctypes.c_int64)]
+        lib.karpo_attn_plan_capacity.restype = ctypes.c_int
+        lib.karpo_attn_workspace_bytes.argtypes = [P(KarpoAttnArgs), P(ctypes.c_size_t)]
+        lib.karpo_attn_workspace_bytes.restype = ctypes.c_int
+        lib.karpo_attn_tile_shape.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, P(ctypes.c_int32),
+                                              P(ctypes.c_int32), P(ctypes.c_int32)]
+        lib.karpo_attn_tile_shape.restype = ctypes.c_int
+        lib.karpo_attn_strerror.argtypes = [ctypes.c_int]
+        lib.karpo_attn_strerror.restype = ctypes.c_char_p
+        lib.karpo_attn_version.argtypes = []
+        lib.karpo_attn_version.restype = ctypes.c_int
+        _lib = lib
+        return lib
+
+
+def message(status: int) -> str:
+    return load().karpo_attn_strerror(status).decode()
+
+
+def check(status: int, what: str) -> None:
+    """Raises for a non-zero status: ValueError for refused arguments, RuntimeError otherwise."""
+    if status == OK:
+        return
+    text = f"{what}: {message(status)} (status {status})"
+    raise (ValueError if status in VALUE_ERRORS else RuntimeError)(text)
+
+
+def tile_shape(heads: int, kv_heads: int, head_dim: int) -> tuple[int, int, int]:
+    """(query rows per tile, keys per step, query heads per work item)."""
+    rows, keys, per = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+    check(load().karpo_attn_tile_shape(heads, kv_heads, head_dim, ctypes.byref(rows), ctypes.byref(keys),
+                                       ctypes.byref(per)), "karpo_attn_tile_shape")
+    return rows.value, keys.value, per.value

@@ -1,0 +1,152 @@
+// The C ABI: argument checks, workspace sizing and the two launches (device planner, attention kernel).
+//
+// Error behaviour follows the reference's host wrapper (families/gemma/triton_attention.py:98-102): unsupported
+// shapes and layouts are refused before anything is launched; here as status codes, which the Python layer turns
+// into ValueError / RuntimeError.
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#include "internal.h"
+#include "karpo_attn.h"
+#include "plan_common.h"
+
+using namespace karpo;
+
+namespace {
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_shape(const KarpoAttnArgs* a) {
+  if (a == nullptr) return KARPO_ATTN_ERR_NULL;
+  if (a->heads < 1 || a->kv_heads < 1 || a->heads % a->kv_heads != 0) return KARPO_ATTN_ERR_HEADS;
+  if (!head_dim_supported(a->head_dim)) return KARPO_ATTN_ERR_HEAD_DIM;
+  if (a->window_left < -1 || a->window_right < -1) return KARPO_ATTN_ERR_WINDOW;
+  if (a->n_seq < 0 || a->total_q < 0 || a->max_q < 0) return KARPO_ATTN_ERR_ARG;
+  return KARPO_ATTN_OK;
+}
+
+// Tiles a launch covers at most: every sequence adds at most one partial tile, and none has more than max_q rows.
+int64_t tile_capacity(const KarpoAttnArgs* a, const Geometry& g) {
+  const int64_t by_rows = (a->total_q + g.rows - 1) / g.rows + a->n_seq;
+  const int64_t by_max = (int64_t)a->n_seq * tiles_of(a->max_q, g.rows);
+  return by_rows < by_max ? by_rows : by_max;
+}
+
+int check_stride(int64_t s) { return s >= 0 && s % 8 == 0; }
+
+}  // namespace
+
+extern "C" int karpo_attn_version(void) { return 1; }
+
+extern "C" const char* karpo_attn_strerror(int status) {
+  switch (status) {
+    case KARPO_ATTN_OK: return "ok";
+    case KARPO_ATTN_ERR_NULL: return "a required pointer is NULL";
+    case KARPO_ATTN_ERR_HEAD_DIM: return "head_dim must be 64, 128 or 256";
+    case KARPO_ATTN_ERR_HEADS: return "heads must be a positive multiple of kv_heads";
+    case KARPO_ATTN_ERR_LAYOUT:
+      return "tensors need a contiguous head dimension, strides that are multiples of 8 elements and 16-byte aligned "
+             "bases";
+    case KARPO_ATTN_ERR_WORKSPACE: return "workspace missing or smaller than karpo_attn_workspace_bytes";
+    case KARPO_ATTN_ERR_WINDOW: return "window sides must be -1 (unbounded) or non-negative";
+    case KARPO_ATTN_ERR_SPANS: return "n_spans must be non-negative, with a spans pointer when positive";
+    case KARPO_ATTN_ERR_LAUNCH: return "the HIP runtime refused a kernel launch";
+    case KARPO_ATTN_ERR_ARG: return "sizes and the sequence count must be non-negative";
+    case KARPO_ATTN_ERR_CAPACITY: return "the plan buffer is smaller than the plan";
+    case KARPO_ATTN_ERR_BOUNDS: return "sequence bounds must be non-negative and non-decreasing";
+    default: return "unknown karpo_attn status";
+  }
+}
+
+extern "C" int karpo_attn_tile_shape(int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t* rows_per_tile,
+                                     int32_t* keys_per_step, int32_t* heads_per_item) {
+  if (heads < 1 || kv_heads < 1 || heads % kv_heads != 0) return KARPO_ATTN_ERR_HEADS;
+  if (!head_dim_supported(head_dim)) return KARPO_ATTN_ERR_HEAD_DIM;
+  const Geometry g = geometry(heads, kv_heads, head_dim);
+  if (rows_per_tile) *rows_per_tile = g.rows;
+  if (keys_per_step) *keys_per_step = g.bn;
+  if (heads_per_item) *heads_per_item = g.ng;
+  return KARPO_ATTN_OK;
+}
+
+extern "C" int karpo_attn_plan_capacity(const KarpoAttnArgs* a, int64_t* entries) {
+  const int st = check_shape(a);
+  if (st != KARPO_ATTN_OK) return st;
+  if (entries == nullptr) return KARPO_ATTN_ERR_NULL;
+  const Geometry g = geometry(a->heads, a->kv_heads, a->head_dim);
+  *entries = kPlanHeader + 2 * tile_capacity(a, g);
+  return KARPO_ATTN_OK;
+}
+
+extern "C" int karpo_attn_workspace_bytes(const KarpoAttnArgs* a, size_t* bytes) {
+  int64_t entries = 0;
+  const int st = karpo_attn_plan_capacity(a, &entries);
+  if (st != KARPO_ATTN_OK) return st;
+  if (bytes == nullptr) return KARPO_ATTN_ERR_NULL;
+  const int64_t ints = entries + (int64_t)a->n_seq + 1;
+  *bytes = (size_t)((ints * 4 + 255) / 256 * 256);
+  return KARPO_ATTN_OK;
+}
+
+extern "C" int karpo_attn_fwd(const KarpoAttnArgs* a, void* stream) {
+  int st = check_shape(a);
+  if (st != KARPO_ATTN_OK) return st;
+  if (a->n_spans < 0 || (a->n_spans > 0 && a->spans == nullptr)) return KARPO_ATTN_ERR_SPANS;
+  if (a->total_q == 0 || a->n_seq == 0) return KARPO_ATTN_OK;  // no query rows: nothing to write
+  if (!a->q || !a->k || !a->v || !a->o || !a->q_cu || !a->k_cu) return KARPO_ATTN_ERR_NULL;
+  if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v) || !aligned16(a->o)) return KARPO_ATTN_ERR_LAYOUT;
+  if (!check_stride(a->q_stride_tok) || !check_stride(a->q_stride_head) || !check_stride(a->k_stride_tok) ||
+      !check_stride(a->k_stride_head) || !check_stride(a->v_stride_tok) || !check_stride(a->v_stride_head) ||
+      !check_stride(a->o_stride_tok) || !check_stride(a->o_stride_head))
+    return KARPO_ATTN_ERR_LAYOUT;
+
+  const Geometry g = geometry(a->heads, a->kv_heads, a->head_dim);
+  const int64_t cap = tile_capacity(a, g);
+  if (cap > (int64_t)INT32_MAX / 4 || cap * g.n_hg > (int64_t)INT32_MAX) return KARPO_ATTN_ERR_ARG;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+
+  const int32_t* plan = a->plan;
+  if (plan == nullptr) {
+    size_t need = 0;
+    karpo_attn_workspace_bytes(a, &need);
+    if (a->workspace == nullptr || a->workspace_bytes < need) return KARPO_ATTN_ERR_WORKSPACE;
+    int32_t* ws = static_cast<int32_t*>(a->workspace);
+    int32_t* tile_base = ws + kPlanHeader + 2 * cap;
+    if (launch_plan(a->q_cu, a->k_cu, a->n_seq, g, a->window_left, a->window_right, ws, (int)cap, tile_base, s) !=
+        hipSuccess)
+      return KARPO_ATTN_ERR_LAUNCH;
+    plan = ws;
+  }
+
+  Params p;
+  memset(&p, 0, sizeof(p));
+  p.q = static_cast<const uint16_t*>(a->q);
+  p.k = static_cast<const uint16_t*>(a->k);
+  p.v = static_cast<const uint16_t*>(a->v);
+  p.o = static_cast<uint16_t*>(a->o);
+  p.sq_t = a->q_stride_tok;
+  p.sq_h = a->q_stride_head;
+  p.sk_t = a->k_stride_tok;
+  p.sk_h = a->k_stride_head;
+  p.sv_t = a->v_stride_tok;
+  p.sv_h = a->v_stride_head;
+  p.so_t = a->o_stride_tok;
+  p.so_h = a->o_stride_head;
+  p.q_cu = a->q_cu;
+  p.k_cu = a->k_cu;
+  p.spans = a->spans;
+  p.n_spans = a->n_spans;
+  p.plan = plan;
+  p.group = a->heads / a->kv_heads;
+  p.ng = g.ng;
+  p.n_hg = g.n_hg;
+  p.left = a->window_left;
+  p.right = a->window_right;
+  // exp2-domain logit factor; a zero scale keeps a tiny positive factor so masked (-inf) logits stay -inf
+  float c = fabsf(a->scale) * 1.4426950408889634f;
+  p.c = c > 1e-30f ? c : 1e-30f;
+  p.qsign = a->scale < 0.f ? 0x80008000u : 0u;
+  if (launch_forward(p, a->head_dim, cap * g.n_hg, s) != hipSuccess) return KARPO_ATTN_ERR_LAUNCH;
+  return KARPO_ATTN_OK;
+}

@@ -1,0 +1,56 @@
+"""Gemma's global-layer hook on MI355X: one HIP launch over every virtual sequence of a pack.
+
+Mirror of src/karpo_decision/families/gemma/triton_attention.py (``supported`` :87-89, ``attend`` :92-110,
+``enable`` :113-125) with the same positional signature, so ``Packed.global_attend`` and its call sites
+(families/gemma/packed.py:242, :245-246, :276-277) take it unchanged. Differences, each a superset:
+
+* causal models are served (the reference's kernel is bidirectional only and ``enable`` refuses causal models):
+  ``attend`` takes keyword-only ``causal``, ``window`` and ``spans``, and ``enable`` installs a causal ``attend`` on a
+  causal model;
+* offsets are 64-bit everywhere, so there is no 131,071-token cap and no 32-bit-offset ValueError;
+* GQA heads share one staged K/V tile instead of re-reading it per query head.
+"""
+
+from __future__ import annotations
+
+import functools
+from typing import Any
+
+import torch
+
+from . import _lib, ops
+
+
+def supported(device: torch.device) -> bool:
+    """A gfx950 (MI355X) GPU and a built library."""
+    if device.type != "cuda" or not torch.cuda.is_available():
+        return False
+    try:
+        _lib.load()
+    except RuntimeError:
+        return False
+    return ops._is_gfx950(device)
+
+
+def attend(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, q_cu: torch.Tensor, k_cu: torch.Tensor,
+           max_q: int, scale: float, *, causal: bool = False, window: int = -1, spans: torch.Tensor | None = None,
+           plan: ops.Plan | None = None) -> torch.Tensor:
+    """Attention per virtual sequence: (Lq, heads, D) bf16 queries over (Lk, kv heads, D) keys and values, sequence
+    i's query rows q_cu[i]:q_cu[i+1] over its key rows k_cu[i]:k_cu[i+1] (int32 on the device), ``max_q`` at least
+    its longest query range; bidirectional unless ``causal`` (aligned at each sequence's end), ``window`` keys before
+    a query's own position (-1: unbounded), ``spans`` (n, 2) int32 query-row ranges that see themselves whole;
+    (Lq, heads, D)."""
+    if torch.is_grad_enabled():
+        raise RuntimeError("hip_attention runs the forward only: call it under torch.inference_mode or no_grad")
+    return ops.run(query, key, value, q_cu, k_cu, max_q, scale, window_left=window, window_right=0 if causal else -1,
+                   spans=spans, plan=plan)
+
+
+def enable(model: Any, max_length: int) -> None:
+    """``attend`` as the global layers' attention of ``model`` (a ``Packed``) for sequences of up to ``max_length``
+    tokens; ValueError where it does not apply (no gfx950 GPU, a non-positive length)."""
+    if not supported(model.lm.embed_tokens.weight.device):
+        raise ValueError("hip_attention needs an MI355X (gfx950) GPU and a built libkarpo_attn.so")
+    if max_length < 1:
+        raise ValueError(f"max_length must be positive, not {max_length}")
+    model.global_attend = functools.partial(attend, causal=True) if model.causal_global else attend

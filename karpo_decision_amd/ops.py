@@ -1,0 +1,170 @@
+"""The packed attention forward as a torch operator (``karpo_amd::packed_attention``) over ``libkarpo_attn.so``.
+
+The operator follows the reference's own pattern for attention kernels (``karpo::fa4_sliding``,
+src/karpo_decision/families/gemma/sliding_attention.py:36-47): a ``torch.library.custom_op`` with no mutated
+arguments and a fake implementation that returns ``query.new_empty(query.shape)``, so it traces and captures like any
+aten op. The callee allocates the output (as triton_attention.py:103 does); inputs are never written; the bounds are
+read on the device when the kernel runs; the launch goes on the current stream of the query's device; nothing syncs.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+from torch import Tensor
+
+from . import _lib
+
+NAMESPACE = "karpo_amd"
+
+
+def _is_gfx950(device: torch.device) -> bool:
+    props = torch.cuda.get_device_properties(device)
+    return getattr(props, "gcnArchName", "").split(":")[0] == "gfx950"
+
+
+def check_inputs(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_cu: Tensor) -> None:
+    """ValueError for anything the kernel does not take (before any launch)."""
+    if query.dim() != 3 or key.dim() != 3 or value.dim() != 3:
+        raise ValueError(f"packed attention takes (rows, heads, head_dim) tensors, got {tuple(query.shape)}, "
+                         f"{tuple(key.shape)}, {tuple(value.shape)}")
+    if key.shape != value.shape:
+        raise ValueError(f"key {tuple(key.shape)} and value {tuple(value.shape)} differ")
+    if query.shape[2] != key.shape[2]:
+        raise ValueError(f"query head_dim {query.shape[2]} != key head_dim {key.shape[2]}")
+    if query.shape[2] not in (64, 128, 256):
+        raise ValueError(f"head_dim must be 64, 128 or 256, not {query.shape[2]}")
+    if key.shape[1] < 1 or query.shape[1] % key.shape[1] != 0:
+        raise ValueError(f"{query.shape[1]} query heads are not a multiple of {key.shape[1]} key/value heads")
+    for name, t in (("query", query), ("key", key), ("value", value)):
+        if t.dtype != torch.bfloat16:
+            raise ValueError(f"{name} must be bfloat16, not {t.dtype} (the kernel computes bf16 MFMA products)")
+        if t.stride(2) != 1 or t.stride(0) % 8 or t.stride(1) % 8:
+            raise ValueError(f"{name} needs a contiguous head_dim and row/head strides that are multiples of 8 "
+                             f"(strides {t.stride()})")
+    for name, t in (("q_cu", q_cu), ("k_cu", k_cu)):
+        if t.dtype != torch.int32 or t.dim() != 1:
+            raise ValueError(f"{name} must be a 1-D int32 tensor, got {t.dtype} {tuple(t.shape)}")
+        if t.device != query.device:
+            raise ValueError(f"{name} is on {t.device}, the query on {query.device}")
+    if q_cu.numel() != k_cu.numel() or q_cu.numel() < 1:
+        raise ValueError(f"q_cu ({q_cu.numel()}) and k_cu ({k_cu.numel()}) must hold the same number of bounds")
+    if key.device != query.device or value.device != query.device:
+        raise ValueError("query, key and value must be on one device")
+
+
+def _args(query: Tensor, key: Tensor, value: Tensor, out: Tensor | None, q_cu: Tensor | None, k_cu: Tensor | None,
+          n_seq: int, max_q: int, scale: float, window_left: int, window_right: int, spans: Tensor | None,
+          plan: Tensor | None) -> _lib.KarpoAttnArgs:
+    a = _lib.KarpoAttnArgs()
+    a.q, a.k, a.v = query.data_ptr(), key.data_ptr(), value.data_ptr()
+    a.o = out.data_ptr() if out is not None else 0
+    a.q_stride_tok, a.q_stride_head = query.stride(0), query.stride(1)
+    a.k_stride_tok, a.k_stride_head = key.stride(0), key.stride(1)
+    a.v_stride_tok, a.v_stride_head = value.stride(0), value.stride(1)
+    if out is not None:
+        a.o_stride_tok, a.o_stride_head = out.stride(0), out.stride(1)
+    a.q_cu = q_cu.data_ptr() if q_cu is not None else 0
+    a.k_cu = k_cu.data_ptr() if k_cu is not None else 0
+    a.n_seq = n_seq
+    a.heads, a.kv_heads, a.head_dim = query.shape[1], key.shape[1], query.shape[2]
+    a.total_q, a.max_q = query.shape[0], max_q
+    a.scale = scale
+    a.window_left, a.window_right = window_left, window_right
+    if spans is not None and spans.numel():
+        a.spans, a.n_spans = spans.data_ptr(), spans.shape[0]
+    a.plan = plan.data_ptr() if plan is not None else 0
+    return a
+
+
+@torch.library.custom_op(f"{NAMESPACE}::packed_attention", mutates_args=())
+def packed_attention(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_cu: Tensor, max_q: int,
+                     scale: float, window_left: int, window_right: int, spans: Tensor | None,
+                     plan: Tensor | None) -> Tensor:
+    """(Tq, heads, D) bf16: sequence i's query rows q_cu[i]:q_cu[i+1] over its key rows k_cu[i]:k_cu[i+1] (bounds
+    int32 on the device), query i at key coordinate i + Lk - Lq, seeing keys j with i' - left <= j <= i' + right
+    (-1: unbounded), or in its own span (``spans`` (n, 2) int32 query-row ranges); ``plan`` a device work list from
+    ``make_plan`` or None (planned on the device)."""
+    check_inputs(query, key, value, q_cu, k_cu)
+    if query.device.type != "cuda":
+        raise ValueError(f"packed attention runs on an MI355X GPU, not on {query.device}")
+    if spans is not None and (spans.dtype != torch.int32 or spans.dim() != 2 or spans.shape[1] != 2
+                              or spans.device != query.device or not spans.is_contiguous()):
+        raise ValueError("spans must be a contiguous (n, 2) int32 tensor on the query's device")
+    if max_q < 0:
+        raise ValueError(f"max_q must be non-negative, not {max_q}")
+    lib = _lib.load()
+    out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
+    if query.shape[0] == 0:
+        return out
+    q_cu, k_cu = q_cu.contiguous(), k_cu.contiguous()
+    with torch.cuda.device(query.device):
+        args = _args(query, key, value, out, q_cu, k_cu, q_cu.numel() - 1, max_q, scale, window_left, window_right,
+                     spans, plan)
+        workspace = None
+        if plan is None:
+            need = ctypes.c_size_t()
+            _lib.check(lib.karpo_attn_workspace_bytes(ctypes.byref(args), ctypes.byref(need)), "packed attention")
+            workspace = torch.empty(need.value, dtype=torch.uint8, device=query.device)
+            args.workspace, args.workspace_bytes = workspace.data_ptr(), need.value
+        stream = torch.cuda.current_stream(query.device).cuda_stream
+        _lib.check(lib.karpo_attn_fwd(ctypes.byref(args), ctypes.c_void_p(stream)), "packed attention")
+    return out
+
+
+@packed_attention.register_fake
+def _(query, key, value, q_cu, k_cu, max_q, scale, window_left, window_right, spans, plan):
+    return query.new_empty(query.shape)
+
+
+@dataclass(frozen=True)
+class Plan:
+    """A pack's work list on the device, built once on the host (like ``block_plan``'s bounds,
+    families/gemma/packed.py:103-151) and reused by every layer of the same head geometry and window."""
+
+    tensor: Tensor
+    heads: int
+    kv_heads: int
+    head_dim: int
+    window_left: int
+    window_right: int
+    tiles: int
+    rows_per_tile: int
+
+
+def make_plan(q_cu: list[int] | Tensor, k_cu: list[int] | Tensor, heads: int, kv_heads: int, head_dim: int,
+              window_left: int = -1, window_right: int = -1, device: torch.device | str = "cuda") -> Plan:
+    """The longest-first work list for host bounds ``q_cu`` / ``k_cu`` (lists or CPU tensors), on ``device``."""
+    qc = [int(x) for x in (q_cu.tolist() if isinstance(q_cu, Tensor) else q_cu)]
+    kc = [int(x) for x in (k_cu.tolist() if isinstance(k_cu, Tensor) else k_cu)]
+    if len(qc) != len(kc) or not qc:
+        raise ValueError("q_cu and k_cu must hold the same, non-zero number of bounds")
+    lib = _lib.load()
+    a = _lib.KarpoAttnArgs()
+    a.heads, a.kv_heads, a.head_dim = heads, kv_heads, head_dim
+    a.window_left, a.window_right = window_left, window_right
+    n = len(qc) - 1
+    rows, _, _ = _lib.tile_shape(heads, kv_heads, head_dim)
+    capacity = 4 + 2 * sum(max(0, -(-(qc[i + 1] - qc[i]) // rows)) for i in range(n))
+    qa = (ctypes.c_int32 * len(qc))(*qc)
+    ka = (ctypes.c_int32 * len(kc))(*kc)
+    buf = (ctypes.c_int32 * capacity)()
+    _lib.check(lib.karpo_attn_plan(ctypes.byref(a), qa, ka, n, buf, capacity), "karpo_attn_plan")
+    host = torch.tensor(list(buf), dtype=torch.int32)
+    return Plan(host.to(device), heads, kv_heads, head_dim, window_left, window_right, int(buf[0]), int(buf[1]))
+
+
+def run(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_cu: Tensor, max_q: int, scale: float,
+        window_left: int = -1, window_right: int = -1, spans: Tensor | None = None,
+        plan: Plan | None = None) -> Tensor:
+    """``packed_attention`` with a ``Plan`` checked against the call's geometry."""
+    tensor = None
+    if plan is not None:
+        if (plan.heads, plan.kv_heads, plan.head_dim, plan.window_left, plan.window_right) != (
+                query.shape[1], key.shape[1], query.shape[2], window_left, window_right):
+            raise ValueError("the plan was made for another head geometry or window")
+        tensor = plan.tensor
+    return packed_attention(query, key, value, q_cu, k_cu, int(max_q), float(scale), int(window_left),
+                            int(window_right), spans, tensor)

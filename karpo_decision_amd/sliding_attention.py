@@ -1,0 +1,28 @@
+"""Gemma's sliding-window layers on MI355X: causal by position, a query sees itself and the ``window`` keys before
+it, over a pack's virtual sequences with separate query and key bounds (a branch's keys are the shared block's tail,
+then its own rows; causal aligned at each sequence's end).
+
+Mirror of src/karpo_decision/families/gemma/sliding_attention.py:85-93 (``attend``); the image soft tokens'
+bidirectional spans that the reference recomputes afterwards with ``vision.see_whole`` (families/gemma/vision.py:
+198-210) are folded into the same launch through ``spans``.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import ops
+
+
+def attend(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, q_cu: torch.Tensor, k_cu: torch.Tensor,
+           max_q: int, max_k: int, scale: float, window: int, *, spans: torch.Tensor | None = None,
+           plan: ops.Plan | None = None) -> torch.Tensor:
+    """(T, heads, D) queries over (Tk, kv heads, D) keys and values (``q_cu`` / ``k_cu``: int32 boundaries), each
+    query seeing at most ``window`` keys before its own position; (T, heads, D). Forward only: RuntimeError when
+    autograd would need a backward."""
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (query, key, value)):
+        raise RuntimeError("sliding_attention on MI355X runs the forward only (no backward kernel)")
+    if window < 0:
+        raise ValueError(f"a sliding window needs a non-negative left size, not {window}")
+    return ops.run(query, key, value, q_cu, k_cu, max_q, scale, window_left=window, window_right=0, spans=spans,
+                   plan=plan)

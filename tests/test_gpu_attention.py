@@ -1,0 +1,360 @@
+"""The HIP kernel against the CPU oracle on an MI355X, through the C ABI (the torch operator and the reference-shaped
+entry points all call karpo_attn_fwd).
+
+Tolerance, bf16 kernel against the fp32 oracle on the same bf16 inputs: max-abs <= 2e-2 and mean-abs <= 2e-3, and
+relative Frobenius error < 1e-2 (tests/gpu/test_triton_attention.py:66). Workloads the oracle cannot finish in
+seconds are compared on sampled query rows (first, last and seeded random rows of every sequence) and heads.
+The edge cases follow the reference's kernel tests (tests/gpu/test_triton_attention.py): one sequence against fp32
+math, a branched varlen pack with an empty virtual sequence, keys past 2^31 elements, bitwise-equal repeated calls,
+large logits; plus every row written (NaN-filled output), device plan == host plan, and graph replays that read
+rewritten bounds.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import golden_io
+from karpo_decision_amd import _lib, global_attention, hip_attention, ops, sliding_attention, varlen, workloads
+from oracle import attention as oa
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS, MEAN_ABS, REL_FRO = 2e-2, 2e-3, 1e-2
+
+
+def assert_close(got: torch.Tensor, want: torch.Tensor, label: str = "") -> dict:
+    got = got.detach().float().cpu()
+    want = want.float().cpu()
+    assert got.shape == want.shape, (got.shape, want.shape)
+    assert torch.isfinite(got).all(), f"{label}: non-finite output"
+    diff = (got - want).abs()
+    stats = {"max_abs": float(diff.max()), "mean_abs": float(diff.mean()),
+             "rel_fro": float((got - want).norm() / want.norm().clamp_min(1e-30))}
+    print(label, stats, flush=True)
+    assert stats["max_abs"] <= MAX_ABS, (label, stats)
+    assert stats["mean_abs"] <= MEAN_ABS, (label, stats)
+    assert stats["rel_fro"] < REL_FRO, (label, stats)
+    return stats
+
+
+def sample_rows(q_cu: list[int], per_seq: int, seed: int) -> list[int]:
+    rng = np.random.default_rng(seed)
+    rows = []
+    for a, b in zip(q_cu[:-1], q_cu[1:]):
+        n = b - a
+        if n == 0:
+            continue
+        edge = list(range(a, min(b, a + 8))) + list(range(max(a, b - 8), b))
+        extra = rng.integers(a, b, size=min(per_seq, n)).tolist()
+        rows.extend(edge + extra)
+    return sorted(set(rows))
+
+
+def run_workload(w: workloads.Workload, plan: ops.Plan | None = None, spans_t=None) -> torch.Tensor:
+    dev = w.query.device
+    q_cu = torch.tensor(w.q_cu, dtype=torch.int32, device=dev)
+    k_cu = torch.tensor(w.k_cu, dtype=torch.int32, device=dev)
+    if spans_t is None and w.spans:
+        spans_t = torch.tensor(w.spans, dtype=torch.int32, device=dev)
+    with torch.inference_mode():
+        return ops.run(w.query, w.key, w.value, q_cu, k_cu, w.max_q, w.scale, w.window_left, w.window_right,
+                       spans_t, plan)
+
+
+def check_workload(w: workloads.Workload, rows=None, groups=None, label=""):
+    """Kernel vs oracle on ``rows`` (all when None) of the query heads of KV heads ``groups`` (all when None)."""
+    got = run_workload(w)
+    torch.cuda.synchronize()
+    q, k, v = w.query, w.key, w.value
+    if groups is not None:
+        g = w.heads // w.kv_heads
+        heads = [kv * g + i for kv in groups for i in range(g)]
+        q, k, v = q[:, heads], k[:, groups], v[:, groups]
+        got = got[:, heads]
+    want = oa.packed_attention(q.cpu(), k.cpu(), v.cpu(), w.q_cu, w.k_cu, w.scale, w.window_left, w.window_right,
+                               w.spans, dtype=torch.float32, rows=rows)
+    if rows is not None:
+        got = got[torch.tensor(rows, device=got.device)]
+    return assert_close(got, want, label or w.name)
+
+
+@pytest.mark.parametrize("name", golden_io.names("random"))
+def test_golden_vectors(gpu, name):
+    c = golden_io.load(name)
+    q, k, v = (c[t].to(gpu, torch.bfloat16) for t in ("q", "k", "v"))
+    q_cu = torch.tensor(c["q_cu"], dtype=torch.int32, device=gpu)
+    k_cu = torch.tensor(c["k_cu"], dtype=torch.int32, device=gpu)
+    spans = torch.tensor(c["spans"], dtype=torch.int32, device=gpu) if c["spans"] else None
+    max_q = max(b - a for a, b in zip(c["q_cu"][:-1], c["q_cu"][1:]))
+    with torch.inference_mode():
+        got = ops.run(q, k, v, q_cu, k_cu, max_q, c["scale"], c["left"], c["right"], spans)
+    assert_close(got, c["want"], name)
+
+
+def test_tiny_workload(gpu):
+    check_workload(workloads.tiny(gpu))
+
+
+def test_tiny_workload_fp32_is_refused(gpu):
+    w = workloads.tiny(gpu, dtype=torch.float32)
+    with pytest.raises(ValueError, match="bfloat16"):
+        run_workload(w)
+
+
+def test_qwen_full_attention_workload(gpu):
+    w = workloads.qwen_full(gpu)
+    check_workload(w)
+
+
+def test_gemma_sliding_workload(gpu):
+    w = workloads.gemma_sliding(gpu)
+    check_workload(w, rows=sample_rows(w.q_cu, 64, 1), groups=[0, 7])
+
+
+def test_gemma_sliding_workload_unit_scale(gpu):
+    """Gemma's own scale is 1.0 (families/gemma/global_attention.py:130-131): logits in the tens."""
+    w = workloads.gemma_sliding(gpu, scale=1.0)
+    check_workload(w, rows=sample_rows(w.q_cu, 32, 2), groups=[1, 6])
+
+
+@pytest.mark.parametrize("length", [32768, 131072])
+def test_gemma_global_workload(gpu, length):
+    w = workloads.gemma_global(length, gpu)
+    check_workload(w, rows=sample_rows(w.q_cu, 384, 3), groups=[0, 15])
+
+
+def test_mixed_multimodal_workload(gpu):
+    w = workloads.mixed_multimodal(gpu)
+    span_rows = [r for s, e in w.spans[:4] for r in (s, s + 1, (s + e) // 2, e - 2, e - 1, e)]
+    rows = sorted(set(sample_rows(w.q_cu, 24, 4) + span_rows))
+    check_workload(w, rows=rows, groups=[0, 2, 15])
+
+
+@pytest.mark.parametrize("heads,kv_heads,head", [(32, 4, 128), (4, 1, 64), (16, 8, 256)])
+def test_one_sequence_matches_float32_math(gpu, heads, kv_heads, head):
+    torch.manual_seed(0)
+    q = (torch.randn(300, heads, head, device=gpu) / 8).bfloat16()
+    k = (torch.randn(300, kv_heads, head, device=gpu) / 8).bfloat16()
+    v = torch.randn(300, kv_heads, head, device=gpu).bfloat16()
+    cu = torch.tensor([0, 300], dtype=torch.int32, device=gpu)
+    with torch.inference_mode():
+        got = hip_attention.attend(q, k, v, cu, cu, 300, 1.0)
+    rep = heads // kv_heads
+    qf, kf, vf = (t.float().transpose(0, 1) for t in (q, k.repeat_interleave(rep, 1), v.repeat_interleave(rep, 1)))
+    want = (torch.softmax(qf @ kf.transpose(1, 2), -1) @ vf).transpose(0, 1)
+    assert_close(got, want.cpu(), f"one-sequence {heads}/{kv_heads}/{head}")
+
+
+@pytest.mark.parametrize("heads,kv_heads,head", [(32, 4, 128), (4, 1, 64)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_branched_varlen_with_an_empty_sequence(gpu, heads, kv_heads, head, causal):
+    """A shared block of 1,000 rows and branches of 37 and 120 rows (each over the shared keys, then its own), and
+    an empty virtual sequence between them (tests/gpu/test_triton_attention.py:69-84)."""
+    torch.manual_seed(1)
+    shared, b1, b2 = 1000, 37, 120
+    n = shared + b1 + b2
+    q = (torch.randn(n, heads, head, device=gpu) / 8).bfloat16()
+    kk = (torch.randn(n, kv_heads, head, device=gpu) / 8).bfloat16()
+    vv = torch.randn(n, kv_heads, head, device=gpu).bfloat16()
+    rows = torch.cat([torch.arange(shared), torch.arange(shared), torch.arange(shared, shared + b1),
+                      torch.arange(shared), torch.arange(shared + b1, n)]).to(gpu)
+    k, v = kk.index_select(0, rows), vv.index_select(0, rows)
+    q_cu = [0, shared, shared + b1, shared + b1, n]
+    k_cu = [0, shared, 2 * shared + b1, 2 * shared + b1, 3 * shared + b1 + b2]
+    with torch.inference_mode():
+        got = hip_attention.attend(q, k, v, torch.tensor(q_cu, dtype=torch.int32, device=gpu),
+                                   torch.tensor(k_cu, dtype=torch.int32, device=gpu), shared, 1.0, causal=causal)
+    want = oa.packed_attention(q.cpu(), k.cpu(), v.cpu(), q_cu, k_cu, 1.0, -1, 0 if causal else -1)
+    assert_close(got, want, f"branched causal={causal}")
+
+
+def test_keys_past_32_bit_offsets(gpu):
+    """Key rows of 16 heads x 128 = 2,048 elements: row 2^20 starts at element 2^31. A first sequence holds 2^20
+    keys and no queries, a second 64 queries over the 300 keys after them (tests/gpu/test_triton_attention.py:93-104)."""
+    torch.manual_seed(2)
+    start, rows, keys = 1 << 20, 64, 300
+    q = (torch.randn(rows, 32, 128, device=gpu) / 8).bfloat16()
+    k = torch.zeros(start + keys, 16, 128, device=gpu, dtype=torch.bfloat16)
+    v = torch.zeros(start + keys, 16, 128, device=gpu, dtype=torch.bfloat16)
+    k[start:] = (torch.randn(keys, 16, 128, device=gpu) / 8).bfloat16()
+    v[start:] = torch.randn(keys, 16, 128, device=gpu).bfloat16()
+    q_cu = torch.tensor([0, 0, rows], dtype=torch.int32, device=gpu)
+    k_cu = torch.tensor([0, start, start + keys], dtype=torch.int32, device=gpu)
+    with torch.inference_mode():
+        got = hip_attention.attend(q, k, v, q_cu, k_cu, rows, 1.0)
+    want = oa.packed_attention(q.cpu(), k[start:].cpu(), v[start:].cpu(), [0, rows], [0, keys], 1.0)
+    assert_close(got, want, "keys past 2^31 elements")
+
+
+@pytest.mark.parametrize("heads,kv_heads,head", [(32, 16, 128), (4, 1, 64), (16, 8, 256)])
+def test_repeated_calls_are_bitwise_equal(gpu, heads, kv_heads, head):
+    torch.manual_seed(3)
+    q = torch.randn(500, heads, head, device=gpu).bfloat16()
+    k = torch.randn(700, kv_heads, head, device=gpu).bfloat16()
+    v = torch.randn(700, kv_heads, head, device=gpu).bfloat16()
+    q_cu = torch.tensor([0, 200, 500], dtype=torch.int32, device=gpu)
+    k_cu = torch.tensor([0, 300, 700], dtype=torch.int32, device=gpu)
+    with torch.inference_mode():
+        a = hip_attention.attend(q, k, v, q_cu, k_cu, 300, 0.1, causal=True)
+        b = hip_attention.attend(q, k, v, q_cu, k_cu, 300, 0.1, causal=True)
+    assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("heads,kv_heads,head", [(32, 4, 128), (4, 1, 64)])
+def test_large_logits_match_float32_math(gpu, heads, kv_heads, head):
+    """Queries and keys without the usual 1/8, at scale 8: logits reach the hundreds, past float32's exp unless the
+    kernel subtracts a running maximum (tests/gpu/test_triton_attention.py:116-128)."""
+    torch.manual_seed(4)
+    q = torch.randn(300, heads, head, device=gpu).bfloat16()
+    k = torch.randn(300, kv_heads, head, device=gpu).bfloat16()
+    v = torch.randn(300, kv_heads, head, device=gpu).bfloat16()
+    cu = torch.tensor([0, 300], dtype=torch.int32, device=gpu)
+    with torch.inference_mode():
+        got = hip_attention.attend(q, k, v, cu, cu, 300, 8.0)
+    want = oa.packed_attention(q.cpu(), k.cpu(), v.cpu(), [0, 300], [0, 300], 8.0)
+    assert_close(got, want, "large logits")
+
+
+def test_negative_and_zero_scale(gpu):
+    torch.manual_seed(5)
+    q = torch.randn(200, 8, 64, device=gpu).bfloat16()
+    k = torch.randn(200, 2, 64, device=gpu).bfloat16()
+    v = torch.randn(200, 2, 64, device=gpu).bfloat16()
+    cu = torch.tensor([0, 80, 200], dtype=torch.int32, device=gpu)
+    for scale in (-0.2, 0.0):
+        with torch.inference_mode():
+            got = ops.run(q, k, v, cu, cu, 120, scale, -1, 0)
+        want = oa.packed_attention(q.cpu(), k.cpu(), v.cpu(), [0, 80, 200], [0, 80, 200], scale, -1, 0)
+        assert_close(got, want, f"scale {scale}")
+
+
+def test_windows_and_spans_on_both_sides(gpu):
+    torch.manual_seed(6)
+    q_cu = [0, 700, 1500, 1510, 2600]
+    q = torch.randn(2600, 16, 128, device=gpu).bfloat16()
+    k = torch.randn(2600, 8, 128, device=gpu).bfloat16()
+    v = torch.randn(2600, 8, 128, device=gpu).bfloat16()
+    spans = [(100, 300), (1000, 1090), (1600, 2160)]
+    st = torch.tensor(spans, dtype=torch.int32, device=gpu)
+    cu = torch.tensor(q_cu, dtype=torch.int32, device=gpu)
+    for left, right in ((200, 0), (-1, 0), (63, 64), (300, -1), (0, 0)):
+        with torch.inference_mode():
+            got = ops.run(q, k, v, cu, cu, 1090, 0.09, left, right, st)
+        want = oa.packed_attention(q.cpu(), k.cpu(), v.cpu(), q_cu, q_cu, 0.09, left, right, spans)
+        assert_close(got, want, f"window ({left}, {right}) with spans")
+
+
+def _c_abi_call(q, k, v, o, q_cu, k_cu, max_q, scale, left, right, plan=None):
+    lib = _lib.load()
+    a = ops._args(q, k, v, o, q_cu, k_cu, q_cu.numel() - 1, max_q, scale, left, right, None, plan)
+    need = ctypes.c_size_t()
+    _lib.check(lib.karpo_attn_workspace_bytes(ctypes.byref(a), ctypes.byref(need)), "workspace")
+    ws = torch.zeros(need.value, dtype=torch.uint8, device=q.device)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), need.value
+    _lib.check(lib.karpo_attn_fwd(ctypes.byref(a), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "fwd")
+    torch.cuda.synchronize()
+    return ws
+
+
+def test_every_row_is_written_and_device_plan_matches_host_plan(gpu):
+    """Through the C ABI: an output pre-filled with NaN has no NaN left; the device planner's work list is the host
+    planner's as a multiset, ordered by non-increasing cost; running from the host plan gives the same bits."""
+    w = workloads.qwen_full(gpu, seed=7)
+    q_cu = torch.tensor(w.q_cu, dtype=torch.int32, device=gpu)
+    o = torch.full_like(w.query, float("nan"))
+    ws = _c_abi_call(w.query, w.key, w.value, o, q_cu, q_cu, w.max_q, w.scale, -1, 0)
+    assert not torch.isnan(o).any()
+    plan = ops.make_plan(w.q_cu, w.k_cu, w.heads, w.kv_heads, w.head_dim, -1, 0, device=gpu)
+    dev = ws.view(torch.int32)[: plan.tensor.numel()].cpu()
+    host = plan.tensor.cpu()
+    assert dev[:4].tolist() == host[:4].tolist()
+    pairs_dev = sorted(map(tuple, dev[4:].view(-1, 2).tolist()))
+    pairs_host = sorted(map(tuple, host[4:].view(-1, 2).tolist()))
+    assert pairs_dev == pairs_host
+    # non-increasing cost along the device list (causal self-attention: steps 0 .. the tile's last row)
+    rows, bn = host[1].item(), host[2].item()
+    costs = []
+    for seg, t in dev[4:].view(-1, 2).tolist():
+        lq = w.q_cu[seg + 1] - w.q_cu[seg]
+        p1 = min(lq, (t + 1) * rows) - 1
+        costs.append(-(-(p1 + 1) // bn) + 1)
+    assert all(a >= b for a, b in zip(costs, costs[1:]))
+    o2 = torch.empty_like(w.query)
+    _c_abi_call(w.query, w.key, w.value, o2, q_cu, q_cu, w.max_q, w.scale, -1, 0, plan=plan.tensor)
+    assert torch.equal(o, o2)
+
+
+def test_reference_shaped_entry_points(gpu):
+    """sliding_attention.attend, varlen.varlen_attn and global_attention.padded against the oracle."""
+    torch.manual_seed(8)
+    q = torch.randn(900, 16, 256, device=gpu).bfloat16()
+    k = torch.randn(1100, 8, 256, device=gpu).bfloat16()
+    v = torch.randn(1100, 8, 256, device=gpu).bfloat16()
+    q_cu, k_cu = [0, 400, 900], [0, 500, 1100]
+    qc, kc = (torch.tensor(x, dtype=torch.int32, device=gpu) for x in (q_cu, k_cu))
+    with torch.inference_mode():
+        got = sliding_attention.attend(q, k, v, qc, kc, 500, 600, 0.0625, 255)
+    assert_close(got, oa.packed_attention(q.cpu(), k.cpu(), v.cpu(), q_cu, k_cu, 0.0625, 255, 0), "sliding")
+
+    q2, k2, v2 = q[:, :, :128].contiguous(), k[:, :, :128].contiguous(), v[:, :, :128].contiguous()
+    with torch.inference_mode():
+        got = varlen.varlen_attn(q2, k2, v2, qc, kc, 500, 600, window_size=(-1, 0), enable_gqa=True)
+    want = oa.packed_attention(q2.cpu(), k2.cpu(), v2.cpu(), q_cu, k_cu, 1 / math.sqrt(128), -1, 0)
+    assert_close(got, want, "varlen causal")
+    with pytest.raises(ValueError, match="enable_gqa"):
+        varlen.varlen_attn(q2, k2, v2, qc, kc, 500, 600)
+
+    cu = torch.tensor([0, 700, 900], dtype=torch.int32, device=gpu)
+    with torch.inference_mode():
+        got = global_attention.padded(q2[None], k2[:900][None], v2[:900][None], cu, 900, True, 0.1)
+    want = oa.packed_attention(q2.cpu(), k2[:900].cpu(), v2[:900].cpu(), [0, 700, 900], [0, 700, 900], 0.1, -1, 0)
+    assert got.shape == (1, 900, 16, 128)
+    assert_close(got[0], want, "padded")
+
+
+def test_graph_replays_read_rewritten_bounds(gpu):
+    """A captured call reads the bounds from device memory at replay time (serve/graphs.py:107-115): rewriting
+    cu in place between replays changes the split, and each replay equals the eager call with those bounds."""
+    torch.manual_seed(9)
+    q = torch.randn(256, 8, 64, device=gpu).bfloat16()
+    k = torch.randn(256, 2, 64, device=gpu).bfloat16()
+    v = torch.randn(256, 2, 64, device=gpu).bfloat16()
+    cu = torch.tensor([0, 100, 256], dtype=torch.int32, device=gpu)
+    with torch.inference_mode():
+        hip_attention.attend(q, k, v, cu, cu, 256, 0.125, causal=True)  # warm: library loaded, allocator primed
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out = hip_attention.attend(q, k, v, cu, cu, 256, 0.125, causal=True)
+        for split in (13, 64, 65, 200, 13):
+            cu[1] = split
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            eager = hip_attention.attend(q, k, v, cu.clone(), cu.clone(), 256, 0.125, causal=True)
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager), split
+            want = oa.packed_attention(q.cpu(), k.cpu(), v.cpu(), [0, split, 256], [0, split, 256], 0.125, -1, 0)
+            assert_close(out, want, f"graph split {split}")
+
+
+def test_enable_installs_the_hook(gpu):
+    import types
+
+    def stub(causal):
+        weight = torch.zeros(1, device=gpu)
+        return types.SimpleNamespace(lm=types.SimpleNamespace(embed_tokens=types.SimpleNamespace(weight=weight)),
+                                     causal_global=causal, global_attend=None)
+
+    m = stub(False)
+    hip_attention.enable(m, 131_072)
+    assert m.global_attend is hip_attention.attend
+    m = stub(True)
+    hip_attention.enable(m, 32_768)
+    assert m.global_attend.keywords == {"causal": True}
