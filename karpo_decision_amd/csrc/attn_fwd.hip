@@ -3,36 +3,67 @@
 // Algorithm (the same arithmetic as the reference's Triton kernel, families/gemma/triton_attention.py:53-84, and the
 // per-sequence SDPA path it replaces, families/gemma/packed.py:195-220): for each query, a running maximum m and sum l
 // in the exp2 domain (logit * scale * log2 e), P = exp2(logit - m) rounded to bf16 for the P.V product, the output
-// accumulated in fp32 and divided by l at the end. Masks (causal / window / image span, varlen alignment of
+// accumulated in fp32 and divided by l at the end. l sums the bf16-rounded P that the P.V product uses, so numerator
+// and denominator carry the same weights. Masks (causal / window / image span, varlen alignment of
 // tests/test_gemma_blocks.py:28-43) are evaluated per element only on key steps that cut through a wave's queries.
 //
-// Data flow of one workgroup (4 waves, one work item = one query tile x one head group):
-//   * each wave holds 32*NB query vectors (position, head) of the tile in registers as MFMA B operands;
-//   * per step, BN keys of K and V are staged in LDS (double buffered; V transposed to [d][key] on the way in);
-//   * S^T = K Q^T on v_mfma_f32_32x32x16_bf16: a lane then owns one query column, so the row max and sum are
-//     in-lane plus one v_permlane32_swap between the two half-waves;
+// Mapping onto a CU: two independent 4-wave workgroups per CU (two waves per SIMD). A wave's exponentials and row
+// reductions run on the VALU while the other workgroup's wave on the same SIMD keeps the matrix core busy, so no
+// in-wave software pipelining is needed. One work item = one query tile x one head group:
+//   * each wave holds 32 query vectors (position, head) of the tile in registers as MFMA B operands;
+//   * per step, BN keys of K and V are copied global -> LDS by the DMA path (global_load_lds, 16 B per lane),
+//     double buffered, the next step's copy in flight while this step computes;
+//   * S^T = K Q^T on v_mfma_f32_32x32x16_bf16: a lane owns one query column, so the row max and sum are in-lane plus
+//     one v_permlane32_swap between the two half-waves;
 //   * K rows are fed to the MFMA in the order that swaps bits 2 and 3 of the row index, which makes each lane's 8
-//     consecutive S^T registers hold 8 consecutive keys: the P registers are directly the B operand of
-//     O^T = V^T P^T, and V^T is read from LDS with one 16-byte read per MFMA;
+//     consecutive S^T registers hold 8 consecutive keys, so the P registers are directly the B operand of
+//     O^T = V^T P^T; the V^T operand comes from the V tile through ds_read_b64_tr_b16;
+//   * LDS tiles are blocked so that every 16 lanes of an LDS read touch one contiguous 256-byte run (conflict-free on
+//     the 64 banks): K as [16-key block][16-byte chunk][16 keys], V as [4-key group][16-wide d block][4 keys][16 d];
+//     every per-step address is a lane base plus an immediate offset;
 //   * the running maximum is only raised when a step's maximum exceeds it by more than 2^8 (exact: the final
 //     division by l cancels any common factor), so O is rescaled on few steps.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
 
-#include "karpo_attn.h"
 #include "internal.h"
+#include "karpo_attn.h"
 #include "plan_common.h"
 
 namespace karpo {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+#define KA_LDS __attribute__((address_space(3)))
+#define KA_GLOBAL __attribute__((address_space(1)))
 
 // Lazy-rescale threshold in log2 units: P values stay below 2^8.
 constexpr float kTau = 8.0f;
+
+// Per head size: keys per step (BN) and workgroups per CU (occupancy).
+template <int D> struct TileCfg;
+template <> struct TileCfg<64> { static constexpr int BN = 64, OCC = 2; };
+template <> struct TileCfg<128> { static constexpr int BN = 64, OCC = 2; };
+template <> struct TileCfg<256> { static constexpr int BN = 32, OCC = 1; };
+
+// Row of the 32-key block that MFMA A-row r reads: bits 2 and 3 of r swapped.
+__device__ __forceinline__ int key_row(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
+
+// Byte offsets inside the LDS tiles.
+//   K: (key k, 16-byte chunk c of its D/8) at ((k / 16) * D/8 + c) * 256 + (k % 16) * 16
+//   V: (key k, element d) at ((k / 4) * D/16 + d / 16) * 128 + (k % 4) * 32 + (d % 16) * 2
+template <int D>
+__device__ __forceinline__ int k_offset(int k, int c) { return ((k >> 4) * (D / 8) + c) * 256 + (k & 15) * 16; }
+template <int D>
+__device__ __forceinline__ int v_offset(int k, int d) {
+  return ((k >> 2) * (D / 16) + (d >> 4)) * 128 + (k & 3) * 32 + (d & 15) * 2;
+}
 
 __device__ __forceinline__ float half_swap_max(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -56,24 +87,38 @@ __device__ __forceinline__ int wave_max(int x) {
   return x;
 }
 
-// Row of the 32-key block that MFMA A-row r reads: bits 2 and 3 of r swapped.
-__device__ __forceinline__ int key_row(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
+// Where lane `lane` of DMA instruction `blk` (1 KiB of the tile each) reads: the key row inside the step and the
+// element column. Inverse of k_offset / v_offset for byte offset blk * 1024 + lane * 16.
+template <int D>
+__device__ __forceinline__ void k_dma_source(int blk, int lane, int* key, int* col) {
+  const int b = blk * 4 + (lane >> 4);  // 256-byte block: (key block, chunk)
+  *key = (b / (D / 8)) * 16 + (lane & 15);
+  *col = (b % (D / 8)) * 8;
+}
+template <int D>
+__device__ __forceinline__ void v_dma_source(int blk, int lane, int* key, int* col) {
+  const int b = blk * 8 + (lane >> 3);  // 128-byte block: (key group, d block)
+  const int piece = lane & 7;
+  *key = (b / (D / 16)) * 4 + (piece >> 1);
+  *col = (b % (D / 16)) * 16 + (piece & 1) * 8;
+}
 
-template <int D, int NB, int BN>
-__global__ __launch_bounds__(kThreads, 1) void attn_fwd_kernel(Params p) {
+template <int D>
+__global__ __launch_bounds__(kThreads, TileCfg<D>::OCC) void attn_fwd_kernel(Params p) {
+  constexpr int BN = TileCfg<D>::BN;
   constexpr int DC = D / 16;       // 16-wide head-dim chunks of the QK^T contraction
   constexpr int DB = D / 32;       // 32-row head-dim blocks of O^T
   constexpr int KB = BN / 32;      // 32-key blocks of S^T
   constexpr int KC = BN / 16;      // 16-key chunks of the PV contraction
-  constexpr int KROW = D + 8;      // LDS pitch of a K row (elements), padded against bank conflicts
-  constexpr int VROW = BN + 8;     // LDS pitch of a V^T row
-  constexpr int R = BN * D / (8 * kThreads);  // 16-byte chunks per thread per step, for K and for V
-  constexpr int KQ = BN / R;       // threads along keys in the V^T staging
-  static_assert(R == 2 || R == 4, "staging assumes 2 or 4 keys per thread");
-  constexpr int VW = 32 * NB;      // query vectors per wave
+  constexpr int TILE = BN * D * 2;  // bytes of one K or V tile
+  constexpr int INSTS = TILE / 1024 / kWaves;  // DMA instructions per wave per tile
+  static_assert(INSTS >= 1, "a tile must give every wave at least one DMA instruction");
 
-  __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][BN * KROW];
-  __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][D * VROW];
+  // separate arrays per buffer: the compiler then sees that a step's copy never writes the tiles it reads
+  __shared__ __attribute__((aligned(1024))) char k_lds0[TILE];
+  __shared__ __attribute__((aligned(1024))) char k_lds1[TILE];
+  __shared__ __attribute__((aligned(1024))) char v_lds0[TILE];
+  __shared__ __attribute__((aligned(1024))) char v_lds1[TILE];
   __shared__ int red[2][kWaves];
 
   const int n_tiles = p.plan[0];
@@ -91,47 +136,42 @@ __global__ __launch_bounds__(kThreads, 1) void attn_fwd_kernel(Params p) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 31, half = lane >> 5;
 
-  // ---- this lane's query vectors: positions, heads, visible key ranges, Q operands
-  int pos[NB], head[NB], lo[NB], hi[NB], sl[NB], sh[NB];
-  bool valid[NB];
+  // ---- this lane's query vector: position, head, visible key ranges
+  const int vec = wave * 32 + col;
+  const int off = vec / p.ng;
+  const int pos = tile * rows_per_tile + off;
+  const int head = hg * p.ng + (vec - off * p.ng);
+  const bool valid = pos < lq;
+  int lo = 0, hi = 0, sl = 0, sh = 0;
   int wlo = INT32_MAX, whi = INT32_MIN, wflo = INT32_MIN, wfhi = INT32_MAX;
-#pragma unroll
-  for (int cb = 0; cb < NB; ++cb) {
-    const int vec = wave * VW + cb * 32 + col;
-    const int off = vec / p.ng;
-    pos[cb] = tile * rows_per_tile + off;
-    head[cb] = hg * p.ng + (vec - off * p.ng);
-    valid[cb] = pos[cb] < lq;
-    lo[cb] = hi[cb] = sl[cb] = sh[cb] = 0;
-    if (valid[cb]) {
-      const int ip = pos[cb] + delta;  // aligned key coordinate
-      int a = p.left < 0 ? 0 : max(0, ip - p.left);
-      int b = p.right < 0 ? lk : (int)min((int64_t)lk, (int64_t)ip + p.right + 1);
-      if (b < a) b = a;
-      lo[cb] = a;
-      hi[cb] = b;
-      wflo = max(wflo, a);
-      wfhi = min(wfhi, b);
-      if (a < b) {
-        wlo = min(wlo, a);
-        whi = max(whi, b);
+  if (valid) {
+    const int ip = pos + delta;  // aligned key coordinate
+    int a = p.left < 0 ? 0 : max(0, ip - p.left);
+    int b = p.right < 0 ? lk : (int)min((int64_t)lk, (int64_t)ip + p.right + 1);
+    if (b < a) b = a;
+    lo = a;
+    hi = b;
+    wflo = a;
+    wfhi = b;
+    if (a < b) {
+      wlo = a;
+      whi = b;
+    }
+    if (p.n_spans > 0) {  // the last span starting at or before this query row
+      const int row = qa + pos;
+      int l0 = 0, l1 = p.n_spans;
+      while (l1 - l0 > 1) {
+        const int mid = (l0 + l1) >> 1;
+        if (p.spans[2 * mid] <= row) l0 = mid; else l1 = mid;
       }
-      if (p.n_spans > 0) {  // the last span starting at or before this query row
-        const int row = qa + pos[cb];
-        int l0 = 0, l1 = p.n_spans;
-        while (l1 - l0 > 1) {
-          const int mid = (l0 + l1) >> 1;
-          if (p.spans[2 * mid] <= row) l0 = mid; else l1 = mid;
-        }
-        const int s0 = p.spans[2 * l0], s1 = p.spans[2 * l0 + 1];
-        if (s0 <= row && row < s1) {
-          const int x = max(0, s0 - qa + delta), y = min(lk, s1 - qa + delta);
-          if (x < y) {
-            sl[cb] = x;
-            sh[cb] = y;
-            wlo = min(wlo, x);
-            whi = max(whi, y);
-          }
+      const int s0 = p.spans[2 * l0], s1 = p.spans[2 * l0 + 1];
+      if (s0 <= row && row < s1) {
+        const int x = max(0, s0 - qa + delta), y = min(lk, s1 - qa + delta);
+        if (x < y) {
+          sl = x;
+          sh = y;
+          wlo = min(wlo, x);
+          whi = max(whi, y);
         }
       }
     }
@@ -145,16 +185,15 @@ __global__ __launch_bounds__(kThreads, 1) void attn_fwd_kernel(Params p) {
     red[1][wave] = whi;
   }
 
-  bf16x8 qop[NB][DC];
-#pragma unroll
-  for (int cb = 0; cb < NB; ++cb) {
-    const uint16_t* qp = p.q + (int64_t)(qa + pos[cb]) * p.sq_t + (int64_t)head[cb] * p.sq_h + half * 8;
+  bf16x8 qop[DC];
+  {
+    const uint16_t* qp = p.q + (int64_t)(qa + pos) * p.sq_t + (int64_t)head * p.sq_h + half * 8;
 #pragma unroll
     for (int dc = 0; dc < DC; ++dc) {
       u32x4 x = {0, 0, 0, 0};
-      if (valid[cb]) x = *(const u32x4*)(qp + dc * 16);
+      if (valid) x = *(const u32x4*)(qp + dc * 16);
       x ^= p.qsign;
-      qop[cb][dc] = __builtin_bit_cast(bf16x8, x);
+      qop[dc] = __builtin_bit_cast(bf16x8, x);
     }
   }
   __syncthreads();
@@ -167,164 +206,135 @@ __global__ __launch_bounds__(kThreads, 1) void attn_fwd_kernel(Params p) {
   const int j_first = klo < khi ? (klo / BN) * BN : 0;
   const int n_steps = klo < khi ? (khi - j_first + BN - 1) / BN : 0;
 
-  // ---- K/V staging: global -> registers (issued a step ahead) -> LDS
+  // ---- DMA sources: per instruction a lane's key row in the step and element column (fixed for the kernel)
   const uint16_t* kbase = p.k + (int64_t)kvh * p.sk_h;
   const uint16_t* vbase = p.v + (int64_t)kvh * p.sv_h;
-  u32x4 kreg[R], vreg[R];
-  const int vkq = tid % KQ, vdq = tid / KQ;
-  auto load_step = [&](int j0) {
+  int k_key[INSTS], k_col[INSTS], v_key[INSTS], v_col[INSTS];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int ci = tid + r * kThreads;
-      const int row = ci / (D / 8), dq = ci % (D / 8);
-      const int key = min(j0 + row, lk - 1);
-      kreg[r] = *(const u32x4*)(kbase + (int64_t)(ka + key) * p.sk_t + dq * 8);
-    }
+  for (int r = 0; r < INSTS; ++r) {
+    k_dma_source<D>(wave * INSTS + r, lane, &k_key[r], &k_col[r]);
+    v_dma_source<D>(wave * INSTS + r, lane, &v_key[r], &v_col[r]);
+  }
+  auto copy_step = [&](int j0, KA_LDS char* kt, KA_LDS char* vt) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int key = min(j0 + vkq * R + r, lk - 1);
-      vreg[r] = *(const u32x4*)(vbase + (int64_t)(ka + key) * p.sv_t + vdq * 8);
-    }
-  };
-  auto store_step = [&](int buf) {
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int ci = tid + r * kThreads;
-      const int row = ci / (D / 8), dq = ci % (D / 8);
-      *(u32x4*)&k_lds[buf][row * KROW + dq * 8] = kreg[r];
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const unsigned sel = (e & 1) ? 0x07060302u : 0x05040100u;
-      uint16_t* dst = &v_lds[buf][(vdq * 8 + e) * VROW + vkq * R];
-      if constexpr (R == 4) {
-        u32x2 w;
-        w[0] = __builtin_amdgcn_perm(vreg[1][e >> 1], vreg[0][e >> 1], sel);
-        w[1] = __builtin_amdgcn_perm(vreg[3][e >> 1], vreg[2][e >> 1], sel);
-        *(u32x2*)dst = w;
-      } else {
-        *(unsigned*)dst = __builtin_amdgcn_perm(vreg[1][e >> 1], vreg[0][e >> 1], sel);
-      }
+    for (int r = 0; r < INSTS; ++r) {
+      const int blk = wave * INSTS + r;
+      const int kk = min(j0 + k_key[r], lk - 1);
+      __builtin_amdgcn_global_load_lds((const KA_GLOBAL void*)(kbase + (int64_t)(ka + kk) * p.sk_t + k_col[r]),
+                                       (KA_LDS void*)(kt + blk * 1024), 16, 0, 0);
+      const int vk = min(j0 + v_key[r], lk - 1);
+      __builtin_amdgcn_global_load_lds((const KA_GLOBAL void*)(vbase + (int64_t)(ka + vk) * p.sv_t + v_col[r]),
+                                       (KA_LDS void*)(vt + blk * 1024), 16, 0, 0);
     }
   };
 
-  f32x16 acc[DB][NB];
+  // ---- LDS read bases (per lane) for the MFMA operands
+  const int k_read = k_offset<D>(key_row(col), half);  // + kb * (2 * D/8 * 256) + dc * 512
+  const int g = lane >> 4, jl = lane & 15;
+  const int v_read = v_offset<D>(8 * (g >> 1) + (jl >> 2), 16 * (g & 1) + 4 * (jl & 3));  // + kc, rr, db offsets
+
+  f32x16 acc[DB];
 #pragma unroll
-  for (int db = 0; db < DB; ++db)
-#pragma unroll
-    for (int cb = 0; cb < NB; ++cb) acc[db][cb] = f32x16{};
-  float m[NB], l[NB];
-#pragma unroll
-  for (int cb = 0; cb < NB; ++cb) {
-    m[cb] = -INFINITY;
-    l[cb] = 0.f;
-  }
+  for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
+  float m = -INFINITY, l = 0.f;
   const float c = p.c;
+  const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
 
-  if (n_steps > 0) {
-    load_step(j_first);
-    store_step(0);
-  }
+  KA_LDS char* const kt0 = (KA_LDS char*)k_lds0;
+  KA_LDS char* const kt1 = (KA_LDS char*)k_lds1;
+  KA_LDS char* const vt0 = (KA_LDS char*)v_lds0;
+  KA_LDS char* const vt1 = (KA_LDS char*)v_lds1;
+  if (n_steps > 0) copy_step(j_first, kt0, vt0);
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
-  for (int s = 0; s < n_steps; ++s) {
-    const int buf = s & 1;
+  // one step: copy the next step's tiles into (kn, vn) while computing on (kt, vt)
+  auto step = [&](int s, const KA_LDS char* kt, const KA_LDS char* vt, KA_LDS char* kn, KA_LDS char* vn) {
     const int j0 = j_first + s * BN;
-    if (s + 1 < n_steps) load_step(j0 + BN);
+    if (s + 1 < n_steps) copy_step(j0 + BN, kn, vn);
     if (j0 < whi && j0 + BN > wlo) {  // wave-uniform: some query of this wave sees a key of this step
-      const uint16_t* kl = k_lds[buf];
-      const uint16_t* vl = v_lds[buf];
-      f32x16 st[KB][NB];
+      f32x16 st[KB];
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-        for (int cb = 0; cb < NB; ++cb) st[kb][cb] = f32x16{};
+      for (int kb = 0; kb < KB; ++kb) st[kb] = f32x16{};
 #pragma unroll
       for (int dc = 0; dc < DC; ++dc) {
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
-          const bf16x8 a = *(const bf16x8*)&kl[(kb * 32 + key_row(col)) * KROW + dc * 16 + half * 8];
-#pragma unroll
-          for (int cb = 0; cb < NB; ++cb)
-            st[kb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qop[cb][dc], st[kb][cb], 0, 0, 0);
+          const bf16x8 a = *(const KA_LDS bf16x8*)(kt + k_read + kb * (2 * (D / 8) * 256) + dc * 512);
+          st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qop[dc], st[kb], 0, 0, 0);
         }
       }
       if (!(j0 >= wflo && j0 + BN <= wfhi)) {  // some query of this wave does not see every key of the step
 #pragma unroll
-        for (int cb = 0; cb < NB; ++cb) {
-#pragma unroll
-          for (int kb = 0; kb < KB; ++kb) {
-#pragma unroll
-            for (int jj = 0; jj < 16; ++jj) {
-              const int key = j0 + kb * 32 + (jj >> 3) * 16 + half * 8 + (jj & 7);
-              const bool vis = (unsigned)(key - lo[cb]) < (unsigned)(hi[cb] - lo[cb]) ||
-                               (unsigned)(key - sl[cb]) < (unsigned)(sh[cb] - sl[cb]);
-              if (!vis) st[kb][cb][jj] = -INFINITY;
-            }
-          }
-        }
-      }
-      float alpha[NB];
-      bool raise = false;
-#pragma unroll
-      for (int cb = 0; cb < NB; ++cb) {
-        float mx = -INFINITY;
-#pragma unroll
-        for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-          for (int jj = 0; jj < 16; ++jj) mx = fmaxf(mx, st[kb][cb][jj]);
-        const float mt = half_swap_max(mx) * c;
-        const bool need = mt > m[cb] + kTau;
-        const float mn = need ? mt : m[cb];
-        alpha[cb] = need ? __builtin_amdgcn_exp2f(m[cb] - mn) : 1.f;
-        raise |= need;
-        m[cb] = mn;
-        l[cb] *= alpha[cb];
-        const float msub = mn == -INFINITY ? 0.f : mn;
-        float sum = 0.f;
-#pragma unroll
         for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
           for (int jj = 0; jj < 16; ++jj) {
-            const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(st[kb][cb][jj], c, -msub));
-            st[kb][cb][jj] = e;
-            sum += e;
+            const int key = j0 + kb * 32 + (jj >> 3) * 16 + half * 8 + (jj & 7);
+            const bool vis = ((unsigned)(key - lo) < (unsigned)(hi - lo)) | ((unsigned)(key - sl) < (unsigned)(sh - sl));
+            st[kb][jj] = vis ? st[kb][jj] : -INFINITY;
           }
-        l[cb] += sum;
       }
-      if (__builtin_amdgcn_ballot_w64(raise)) {
+      float mx = -INFINITY;
 #pragma unroll
-        for (int db = 0; db < DB; ++db)
+      for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-          for (int cb = 0; cb < NB; ++cb) acc[db][cb] *= alpha[cb];
+        for (int jj = 0; jj < 16; ++jj) mx = fmaxf(mx, st[kb][jj]);
+      const float mt = half_swap_max(mx) * c;
+      const bool need = mt > m + kTau;
+      if (__builtin_amdgcn_ballot_w64(need)) {  // raise the running maximum (rare after the first steps)
+        const float mn = need ? mt : m;
+        const float alpha = need ? __builtin_amdgcn_exp2f(m - mn) : 1.f;  // m = -inf, mt finite: alpha = 0
+        m = mn;
+        l *= alpha;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) acc[db] *= alpha;
       }
+      const float msub = m == -INFINITY ? 0.f : m;
+      bf16x8 pb[KC];
+      float part[2] = {0.f, 0.f};
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc) {
-        bf16x8 pb[NB];
 #pragma unroll
-        for (int cb = 0; cb < NB; ++cb)
+        for (int t = 0; t < 8; t += 2) {
+          const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[kc >> 1][(kc & 1) * 8 + t], c, -msub));
+          const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[kc >> 1][(kc & 1) * 8 + t + 1], c, -msub));
+          const bf16x2 pr = {(__bf16)e0, (__bf16)e1};
+          pb[kc][t] = pr[0];
+          pb[kc][t + 1] = pr[1];
+          part[(t >> 1) & 1] = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, part[(t >> 1) & 1], false);
+        }
+      }
+      l += part[0] + part[1];
 #pragma unroll
-          for (int t = 0; t < 8; ++t) pb[cb][t] = (__bf16)st[kc >> 1][cb][(kc & 1) * 8 + t];
+      for (int kc = 0; kc < KC; ++kc) {
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
-          const bf16x8 a = *(const bf16x8*)&vl[(db * 32 + col) * VROW + kc * 16 + half * 8];
+          bf16x4 pv[2];
 #pragma unroll
-          for (int cb = 0; cb < NB; ++cb)
-            acc[db][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[cb], acc[db][cb], 0, 0, 0);
+          for (int rr = 0; rr < 2; ++rr)
+            pv[rr] = __builtin_bit_cast(
+                bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                            (KA_LDS s16x4*)(vt + v_read + (kc * 4 + rr) * (D / 16) * 128 + db * 256)));
+          const bf16x8 a = __builtin_shufflevector(pv[0], pv[1], 0, 1, 2, 3, 4, 5, 6, 7);
+          acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[kc], acc[db], 0, 0, 0);
         }
       }
     }
-    if (s + 1 < n_steps) store_step(buf ^ 1);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+  };
+  int s = 0;
+  for (; s + 1 < n_steps; s += 2) {
+    step(s, kt0, vt0, kt1, vt1);
+    step(s + 1, kt1, vt1, kt0, vt0);
   }
+  if (s < n_steps) step(s, kt0, vt0, kt1, vt1);
 
   // ---- normalise and store: lane (col, half) holds d = db*32 + (j/4)*8 + half*4 + j%4 of its query
-#pragma unroll
-  for (int cb = 0; cb < NB; ++cb) {
-    const float lt = half_swap_sum(l[cb]);
-    const float inv = lt > 0.f ? 1.f / lt : 0.f;
-    if (!valid[cb]) continue;
-    uint16_t* op = p.o + (int64_t)(qa + pos[cb]) * p.so_t + (int64_t)head[cb] * p.so_h + half * 4;
+  const float lt = half_swap_sum(l);
+  const float inv = lt > 0.f ? 1.f / lt : 0.f;
+  if (valid) {
+    uint16_t* op = p.o + (int64_t)(qa + pos) * p.so_t + (int64_t)head * p.so_h + half * 4;
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
 #pragma unroll
@@ -332,8 +342,8 @@ __global__ __launch_bounds__(kThreads, 1) void attn_fwd_kernel(Params p) {
         u32x2 w;
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-          const __bf16 x0 = (__bf16)(acc[db][cb][g4 * 4 + 2 * t] * inv);
-          const __bf16 x1 = (__bf16)(acc[db][cb][g4 * 4 + 2 * t + 1] * inv);
+          const __bf16 x0 = (__bf16)(acc[db][g4 * 4 + 2 * t] * inv);
+          const __bf16 x1 = (__bf16)(acc[db][g4 * 4 + 2 * t + 1] * inv);
           w[t] = (unsigned)__builtin_bit_cast(uint16_t, x0) | ((unsigned)__builtin_bit_cast(uint16_t, x1) << 16);
         }
         *(u32x2*)(op + db * 32 + g4 * 8) = w;
@@ -448,18 +458,18 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* __res
 // ---- launch
 
 
-template <int D, int NB, int BN>
+template <int D>
 static hipError_t launch_attn(const Params& p, int64_t grid, hipStream_t stream) {
-  hipLaunchKernelGGL((attn_fwd_kernel<D, NB, BN>), dim3((unsigned)grid), dim3(kThreads), 0, stream, p);
+  hipLaunchKernelGGL((attn_fwd_kernel<D>), dim3((unsigned)grid), dim3(kThreads), 0, stream, p);
   return hipGetLastError();
 }
 
 hipError_t launch_forward(const Params& p, int head_dim, int64_t grid, hipStream_t stream) {
   if (grid <= 0) return hipSuccess;
   switch (head_dim) {
-    case 64: return launch_attn<64, 2, 64>(p, grid, stream);
-    case 128: return launch_attn<128, 2, 64>(p, grid, stream);
-    case 256: return launch_attn<256, 1, 32>(p, grid, stream);
+    case 64: return launch_attn<64>(p, grid, stream);
+    case 128: return launch_attn<128>(p, grid, stream);
+    case 256: return launch_attn<256>(p, grid, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -1,7 +1,7 @@
 // Tile geometry and the per-tile cost shared by the host planner (plan.cpp) and the device planner (attn_fwd.hip).
 //
-// A work item is one query tile of one segment for one group of query heads. A tile holds `vectors` query vectors
-// (vectors = 128 * NB, NB = 2 for head_dim <= 128, 1 for 256); a vector is one (position, head) pair. When the GQA
+// A work item is one query tile of one segment for one group of query heads. A tile holds 128 query vectors (32 per
+// wave of a 4-wave workgroup); a vector is one (position, head) pair. When the GQA
 // group size G divides `vectors`, a tile covers vectors / G positions of all G heads of one key/value head, so one
 // staged K/V tile serves every head of the group; otherwise a tile covers `vectors` positions of one query head.
 #pragma once
@@ -21,7 +21,6 @@ constexpr int kPlanHeader = 4;       // int32 header of a plan: tiles, rows per 
 constexpr int kCostBuckets = 2048;   // device planner's cost histogram (costs clamp to the last bucket)
 
 struct Geometry {
-  int nb;        // 32-vector column blocks per wave
   int vectors;   // query vectors per tile
   int bn;        // keys per step
   int ng;        // query heads per work item
@@ -33,8 +32,7 @@ KA_HD inline bool head_dim_supported(int d) { return d == 64 || d == 128 || d ==
 
 KA_HD inline Geometry geometry(int heads, int kv_heads, int head_dim) {
   Geometry g;
-  g.nb = head_dim <= 128 ? 2 : 1;
-  g.vectors = 32 * g.nb * kWaves;
+  g.vectors = 32 * kWaves;
   g.bn = head_dim <= 128 ? 64 : 32;
   int group = heads / kv_heads;
   g.ng = (g.vectors % group == 0) ? group : 1;

@@ -89,7 +89,9 @@ def packed_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor
         vs = v[ka:kb].index_select(1, kv_index).transpose(0, 1)[None]
         q_id, k_id = span_ids(qa, lq, lk, spans)
         has_span = bool((q_id >= 0).any())
-        plain_causal = window_left < 0 and window_right == 0 and lq == lk and not has_span and want is None
+        # torch's CPU is_causal path is only used for positive scales (with a negative scale it returns NaN)
+        plain_causal = (window_left < 0 and window_right == 0 and lq == lk and not has_span and want is None
+                        and scale > 0)
         if lk == 0:
             continue
         if plain_causal:

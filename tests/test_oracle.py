@@ -115,6 +115,15 @@ def test_scale_multiplies_the_logits():
     torch.testing.assert_close(a, c, atol=1e-12, rtol=0)
 
 
+@pytest.mark.parametrize("left,right", [(-1, 0), (4, 0), (-1, -1)])
+def test_negative_and_zero_scales_under_masks(left, right):
+    q, k, v, q_cu, k_cu = _pack([12, 9], [12, 9], 4, 2, 8, seed=9)
+    for scale in (-0.3, 0.0):
+        got = oa.packed_attention(q, k, v, q_cu, k_cu, scale, left, right, dtype=torch.float64)
+        want = brute.attention(q.numpy(), k.numpy(), v.numpy(), q_cu, k_cu, scale, left, right)
+        np.testing.assert_allclose(got.numpy(), want, atol=1e-12, rtol=1e-12)
+
+
 def test_a_planted_mask_mistake_is_caught():
     """The checks above must reject a plausible oracle bug: alignment at the start instead of the end of the keys."""
     c = golden_io.load("mask_window_bottom_right")

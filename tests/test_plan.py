@@ -70,11 +70,11 @@ def test_host_plan_matches_brute_force(q_lens, extra, geom, left, right):
 
 
 def test_tile_geometry():
-    # a tile holds 256 query vectors (128 at head_dim 256): the GQA group's heads share it when they divide it
-    assert _lib.tile_shape(32, 16, 128) == (128, 64, 2)
-    assert _lib.tile_shape(8, 2, 64) == (64, 64, 4)
+    # a tile holds 128 query vectors: the GQA group's heads share it when they divide it
+    assert _lib.tile_shape(32, 16, 128) == (64, 64, 2)
+    assert _lib.tile_shape(8, 2, 64) == (32, 64, 4)
     assert _lib.tile_shape(16, 8, 256) == (64, 32, 2)
-    assert _lib.tile_shape(12, 4, 128) == (256, 64, 1)  # group of 3: one head per item
+    assert _lib.tile_shape(12, 4, 128) == (128, 64, 1)  # group of 3: one head per item
 
 
 def test_plan_refuses_bad_bounds_and_small_buffers():
@@ -144,7 +144,7 @@ def test_workspace_and_capacity():
 
 def test_python_plan_object():
     plan = ops.make_plan([0, 100, 400], [0, 100, 400], 32, 16, 128, -1, 0, device="cpu")
-    assert plan.tiles == 1 + 3 and plan.rows_per_tile == 128
+    assert plan.tiles == 2 + 5 and plan.rows_per_tile == 64
     assert plan.tensor.dtype.is_signed and plan.tensor.numel() == 4 + 2 * plan.tiles
 
 
