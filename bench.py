@@ -39,6 +39,9 @@ def parse() -> argparse.Namespace:
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-repeats", type=int, default=3)
+    p.add_argument("--copy-bytes", type=int, default=0,
+                   help="after the timed steps, copy this many bytes device to device once (a calibration kernel of "
+                        "known traffic for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     return p.parse_args()
 
 
@@ -126,6 +129,13 @@ def main() -> int:
             b.record(stream)
         end.record(stream)
         torch.cuda.synchronize()
+    if args.copy_bytes:
+        src = torch.ones(args.copy_bytes // 4, dtype=torch.float32, device=device)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     total_ms = begin.elapsed_time(end)
     launch_ms = statistics.mean(a.elapsed_time(b) for a, b in marks)
     ms_per_step = total_ms / args.steps

@@ -45,6 +45,8 @@ typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 
 // Lazy-rescale threshold in log2 units: P values stay below 2^8.
 constexpr float kTau = 8.0f;
+// Buffer resource word 3 for raw 32-bit accesses (bounds-checked against num_records, zero past the end).
+constexpr int kBufferFlags = 0x00020000;
 
 // Per head size: keys per step (BN) and workgroups per CU (occupancy).
 template <int D> struct TileCfg;
@@ -103,6 +105,12 @@ __device__ __forceinline__ void v_dma_source(int blk, int lane, int* key, int* c
   *col = (b % (D / 16)) * 16 + (piece & 1) * 8;
 }
 
+// One 16-byte chunk per lane from `base + voff` (bounds-checked against `bytes`: zeros past it) to `lds + 16 * lane`.
+__device__ __forceinline__ void dma_16b(const uint16_t* base, int bytes, KA_LDS char* lds, uint32_t voff) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, bytes, kBufferFlags);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (KA_LDS void*)lds, 16, voff, 0, 0, 0);
+}
+
 template <int D>
 __global__ __launch_bounds__(kThreads, TileCfg<D>::OCC) void attn_fwd_kernel(Params p) {
   constexpr int BN = TileCfg<D>::BN;
@@ -133,7 +141,8 @@ __global__ __launch_bounds__(kThreads, TileCfg<D>::OCC) void attn_fwd_kernel(Par
   const int delta = lk - lq;
   const int kvh = (hg * p.ng) / p.group;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 31, half = lane >> 5;
 
   // ---- this lane's query vector: position, head, visible key ranges
@@ -176,10 +185,10 @@ __global__ __launch_bounds__(kThreads, TileCfg<D>::OCC) void attn_fwd_kernel(Par
       }
     }
   }
-  wlo = wave_min(wlo);
-  whi = wave_max(whi);
-  wflo = wave_max(wflo);
-  wfhi = wave_min(wfhi);
+  wlo = __builtin_amdgcn_readfirstlane(wave_min(wlo));
+  whi = __builtin_amdgcn_readfirstlane(wave_max(whi));
+  wflo = __builtin_amdgcn_readfirstlane(wave_max(wflo));
+  wfhi = __builtin_amdgcn_readfirstlane(wave_min(wfhi));
   if (lane == 0) {
     red[0][wave] = wlo;
     red[1][wave] = whi;
@@ -203,28 +212,34 @@ __global__ __launch_bounds__(kThreads, TileCfg<D>::OCC) void attn_fwd_kernel(Par
     klo = min(klo, red[0][w]);
     khi = max(khi, red[1][w]);
   }
+  klo = __builtin_amdgcn_readfirstlane(klo);
+  khi = __builtin_amdgcn_readfirstlane(khi);
   const int j_first = klo < khi ? (klo / BN) * BN : 0;
   const int n_steps = klo < khi ? (khi - j_first + BN - 1) / BN : 0;
 
-  // ---- DMA sources: per instruction a lane's key row in the step and element column (fixed for the kernel)
-  const uint16_t* kbase = p.k + (int64_t)kvh * p.sk_h;
-  const uint16_t* vbase = p.v + (int64_t)kvh * p.sv_h;
-  int k_key[INSTS], k_col[INSTS], v_key[INSTS], v_col[INSTS];
+  // ---- DMA: per instruction a lane's byte offset inside the step's rows (fixed for the kernel). Each step's rows
+  // are one buffer resource starting at the step's first key row, sized to the rows that exist: reads past the
+  // sequence's last key return zeros, so no per-step address arithmetic runs on the VALU.
+  const uint16_t* kbase = p.k + (int64_t)kvh * p.sk_h + (int64_t)ka * p.sk_t;
+  const uint16_t* vbase = p.v + (int64_t)kvh * p.sv_h + (int64_t)ka * p.sv_t;
+  uint32_t k_voff[INSTS], v_voff[INSTS];
 #pragma unroll
   for (int r = 0; r < INSTS; ++r) {
-    k_dma_source<D>(wave * INSTS + r, lane, &k_key[r], &k_col[r]);
-    v_dma_source<D>(wave * INSTS + r, lane, &v_key[r], &v_col[r]);
+    int key, colm;
+    k_dma_source<D>(wave * INSTS + r, lane, &key, &colm);
+    k_voff[r] = (uint32_t)(key * p.sk_t + colm) * 2u;
+    v_dma_source<D>(wave * INSTS + r, lane, &key, &colm);
+    v_voff[r] = (uint32_t)(key * p.sv_t + colm) * 2u;
   }
   auto copy_step = [&](int j0, KA_LDS char* kt, KA_LDS char* vt) {
+    const int rows = min(lk - j0, BN);
+    const uint16_t* ks = kbase + (int64_t)j0 * p.sk_t;
+    const uint16_t* vs = vbase + (int64_t)j0 * p.sv_t;
 #pragma unroll
     for (int r = 0; r < INSTS; ++r) {
       const int blk = wave * INSTS + r;
-      const int kk = min(j0 + k_key[r], lk - 1);
-      __builtin_amdgcn_global_load_lds((const KA_GLOBAL void*)(kbase + (int64_t)(ka + kk) * p.sk_t + k_col[r]),
-                                       (KA_LDS void*)(kt + blk * 1024), 16, 0, 0);
-      const int vk = min(j0 + v_key[r], lk - 1);
-      __builtin_amdgcn_global_load_lds((const KA_GLOBAL void*)(vbase + (int64_t)(ka + vk) * p.sv_t + v_col[r]),
-                                       (KA_LDS void*)(vt + blk * 1024), 16, 0, 0);
+      dma_16b(ks, rows * (int)p.sk_t * 2, kt + blk * 1024, k_voff[r]);
+      dma_16b(vs, rows * (int)p.sv_t * 2, vt + blk * 1024, v_voff[r]);
     }
   };
 

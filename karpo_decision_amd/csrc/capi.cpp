@@ -102,6 +102,10 @@ extern "C" int karpo_attn_fwd(const KarpoAttnArgs* a, void* stream) {
     return KARPO_ATTN_ERR_LAYOUT;
 
   const Geometry g = geometry(a->heads, a->kv_heads, a->head_dim);
+  // a step's key rows are addressed with 32-bit byte offsets
+  if ((a->k_stride_tok + a->head_dim) * g.bn * 2 >= (int64_t)INT32_MAX ||
+      (a->v_stride_tok + a->head_dim) * g.bn * 2 >= (int64_t)INT32_MAX)
+    return KARPO_ATTN_ERR_LAYOUT;
   const int64_t cap = tile_capacity(a, g);
   if (cap > (int64_t)INT32_MAX / 4 || cap * g.n_hg > (int64_t)INT32_MAX) return KARPO_ATTN_ERR_ARG;
   hipStream_t s = static_cast<hipStream_t>(stream);
