@@ -50,9 +50,10 @@ constexpr int kBufferFlags = 0x00020000;
 
 // Per head size: keys per step (BN) and workgroups per CU (occupancy).
 template <int D> struct TileCfg;
-template <> struct TileCfg<64> { static constexpr int BN = 64, OCC = 2; };
-template <> struct TileCfg<128> { static constexpr int BN = 64, OCC = 2; };
-template <> struct TileCfg<256> { static constexpr int BN = 32, OCC = 1; };
+template <> struct TileCfg<64> { static constexpr int BN = 64, OCC = 2, NBUF = 2; };
+// 32 keys per step keep a wave at 148 VGPRs: three workgroups per CU (the measured best on the 32k causal layer)
+template <> struct TileCfg<128> { static constexpr int BN = 32, OCC = 3, NBUF = 2; };
+template <> struct TileCfg<256> { static constexpr int BN = 32, OCC = 1, NBUF = 2; };
 
 // Row of the 32-key block that MFMA A-row r reads: bits 2 and 3 of r swapped.
 __device__ __forceinline__ int key_row(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
@@ -105,6 +106,13 @@ __device__ __forceinline__ void v_dma_source(int blk, int lane, int* key, int* c
   *col = (b % (D / 16)) * 16 + (piece & 1) * 8;
 }
 
+// s_waitcnt vmcnt(N) (expcnt and lgkmcnt not waited on): at most N vector-memory operations of this wave in flight.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit field");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 // One 16-byte chunk per lane from `base + voff` (bounds-checked against `bytes`: zeros past it) to `lds + 16 * lane`.
 __device__ __forceinline__ void dma_16b(const uint16_t* base, int bytes, KA_LDS char* lds, uint32_t voff) {
   const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, bytes, kBufferFlags);
@@ -123,10 +131,14 @@ __global__ __launch_bounds__(kThreads, TileCfg<D>::OCC) void attn_fwd_kernel(Par
   static_assert(INSTS >= 1, "a tile must give every wave at least one DMA instruction");
 
   // separate arrays per buffer: the compiler then sees that a step's copy never writes the tiles it reads
+  constexpr int NBUF = TileCfg<D>::NBUF;
+  static_assert(NBUF == 2 || NBUF == 3, "two or three K/V buffers");
   __shared__ __attribute__((aligned(1024))) char k_lds0[TILE];
   __shared__ __attribute__((aligned(1024))) char k_lds1[TILE];
+  __shared__ __attribute__((aligned(1024))) char k_lds2[NBUF > 2 ? TILE : 16];
   __shared__ __attribute__((aligned(1024))) char v_lds0[TILE];
   __shared__ __attribute__((aligned(1024))) char v_lds1[TILE];
+  __shared__ __attribute__((aligned(1024))) char v_lds2[NBUF > 2 ? TILE : 16];
   __shared__ int red[2][kWaves];
 
   const int n_tiles = p.plan[0];
@@ -231,16 +243,21 @@ __global__ __launch_bounds__(kThreads, TileCfg<D>::OCC) void attn_fwd_kernel(Par
     v_dma_source<D>(wave * INSTS + r, lane, &key, &colm);
     v_voff[r] = (uint32_t)(key * p.sv_t + colm) * 2u;
   }
-  auto copy_step = [&](int j0, KA_LDS char* kt, KA_LDS char* vt) {
+  auto copy_k = [&](int j0, KA_LDS char* kt) {
     const int rows = min(lk - j0, BN);
     const uint16_t* ks = kbase + (int64_t)j0 * p.sk_t;
+#pragma unroll
+    for (int r = 0; r < INSTS; ++r) dma_16b(ks, rows * (int)p.sk_t * 2, kt + (wave * INSTS + r) * 1024, k_voff[r]);
+  };
+  auto copy_v = [&](int j0, KA_LDS char* vt) {
+    const int rows = min(lk - j0, BN);
     const uint16_t* vs = vbase + (int64_t)j0 * p.sv_t;
 #pragma unroll
-    for (int r = 0; r < INSTS; ++r) {
-      const int blk = wave * INSTS + r;
-      dma_16b(ks, rows * (int)p.sk_t * 2, kt + blk * 1024, k_voff[r]);
-      dma_16b(vs, rows * (int)p.sv_t * 2, vt + blk * 1024, v_voff[r]);
-    }
+    for (int r = 0; r < INSTS; ++r) dma_16b(vs, rows * (int)p.sv_t * 2, vt + (wave * INSTS + r) * 1024, v_voff[r]);
+  };
+  auto copy_step = [&](int j0, KA_LDS char* kt, KA_LDS char* vt) {
+    copy_k(j0, kt);
+    copy_v(j0, vt);
   };
 
   // ---- LDS read bases (per lane) for the MFMA operands
@@ -257,16 +274,20 @@ __global__ __launch_bounds__(kThreads, TileCfg<D>::OCC) void attn_fwd_kernel(Par
 
   KA_LDS char* const kt0 = (KA_LDS char*)k_lds0;
   KA_LDS char* const kt1 = (KA_LDS char*)k_lds1;
+  KA_LDS char* const kt2 = (KA_LDS char*)k_lds2;
   KA_LDS char* const vt0 = (KA_LDS char*)v_lds0;
   KA_LDS char* const vt1 = (KA_LDS char*)v_lds1;
+  KA_LDS char* const vt2 = (KA_LDS char*)v_lds2;
+  // prologue: the first NBUF - 1 steps in flight, wait for the first
   if (n_steps > 0) copy_step(j_first, kt0, vt0);
-  __builtin_amdgcn_s_waitcnt(0);
+  if (NBUF > 2 && n_steps > 1) copy_step(j_first + BN, kt1, vt1);
+  if (NBUF > 2 && n_steps > 1) wait_vmcnt<2 * INSTS>(); else wait_vmcnt<0>();
   __syncthreads();
 
-  // one step: copy the next step's tiles into (kn, vn) while computing on (kt, vt)
+  // step s: copy step s + NBUF - 1 into (kn, vn) while computing on (kt, vt); then wait for step s + 1's copy
   auto step = [&](int s, const KA_LDS char* kt, const KA_LDS char* vt, KA_LDS char* kn, KA_LDS char* vn) {
     const int j0 = j_first + s * BN;
-    if (s + 1 < n_steps) copy_step(j0 + BN, kn, vn);
+    if (s + NBUF - 1 < n_steps) copy_step(j0 + (NBUF - 1) * BN, kn, vn);
     if (j0 < whi && j0 + BN > wlo) {  // wave-uniform: some query of this wave sees a key of this step
       f32x16 st[KB];
 #pragma unroll
@@ -335,15 +356,27 @@ __global__ __launch_bounds__(kThreads, TileCfg<D>::OCC) void attn_fwd_kernel(Par
         }
       }
     }
-    __builtin_amdgcn_s_waitcnt(0);
+    // copies issued after step s + 1's: min(NBUF - 2, n_steps - 2 - s); only a full set may stay in flight
+    if (NBUF > 2 && n_steps - 2 - s >= NBUF - 2) wait_vmcnt<2 * INSTS * (NBUF - 2)>(); else wait_vmcnt<0>();
     __syncthreads();
   };
   int s = 0;
-  for (; s + 1 < n_steps; s += 2) {
-    step(s, kt0, vt0, kt1, vt1);
-    step(s + 1, kt1, vt1, kt0, vt0);
+  if constexpr (NBUF == 2) {
+    for (; s + 1 < n_steps; s += 2) {
+      step(s, kt0, vt0, kt1, vt1);
+      step(s + 1, kt1, vt1, kt0, vt0);
+    }
+    if (s < n_steps) step(s, kt0, vt0, kt1, vt1);
+  } else {
+    for (; s + 2 < n_steps; s += 3) {
+      step(s, kt0, vt0, kt2, vt2);
+      step(s + 1, kt1, vt1, kt0, vt0);
+      step(s + 2, kt2, vt2, kt1, vt1);
+    }
+    if (s < n_steps) step(s, kt0, vt0, kt2, vt2);
+    if (s + 1 < n_steps) step(s + 1, kt1, vt1, kt0, vt0);
   }
-  if (s < n_steps) step(s, kt0, vt0, kt1, vt1);
+
 
   // ---- normalise and store: lane (col, half) holds d = db*32 + (j/4)*8 + half*4 + j%4 of its query
   const float lt = half_swap_sum(l);

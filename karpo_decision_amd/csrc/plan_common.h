@@ -33,7 +33,7 @@ KA_HD inline bool head_dim_supported(int d) { return d == 64 || d == 128 || d ==
 KA_HD inline Geometry geometry(int heads, int kv_heads, int head_dim) {
   Geometry g;
   g.vectors = 32 * kWaves;
-  g.bn = head_dim <= 128 ? 64 : 32;
+  g.bn = head_dim <= 64 ? 64 : 32;  // keys per step of the kernel for this head size
   int group = heads / kv_heads;
   g.ng = (g.vectors % group == 0) ? group : 1;
   g.rows = g.vectors / g.ng;

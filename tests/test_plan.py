@@ -71,10 +71,10 @@ def test_host_plan_matches_brute_force(q_lens, extra, geom, left, right):
 
 def test_tile_geometry():
     # a tile holds 128 query vectors: the GQA group's heads share it when they divide it
-    assert _lib.tile_shape(32, 16, 128) == (64, 64, 2)
+    assert _lib.tile_shape(32, 16, 128) == (64, 32, 2)
     assert _lib.tile_shape(8, 2, 64) == (32, 64, 4)
     assert _lib.tile_shape(16, 8, 256) == (64, 32, 2)
-    assert _lib.tile_shape(12, 4, 128) == (128, 64, 1)  # group of 3: one head per item
+    assert _lib.tile_shape(12, 4, 128) == (128, 32, 1)  # group of 3: one head per item
 
 
 def test_plan_refuses_bad_bounds_and_small_buffers():
