@@ -48,12 +48,11 @@ constexpr float kTau = 8.0f;
 // Buffer resource word 3 for raw 32-bit accesses (bounds-checked against num_records, zero past the end).
 constexpr int kBufferFlags = 0x00020000;
 
-// Per head size: keys per step (BN) and workgroups per CU (occupancy).
+// Per head size: keys per step (BN), workgroups per CU (occupancy; registers and LDS both fit it) and K/V buffers.
 template <int D> struct TileCfg;
-template <> struct TileCfg<64> { static constexpr int BN = 64, OCC = 2, NBUF = 2; };
-// 32 keys per step keep a wave at 148 VGPRs: three workgroups per CU (the measured best on the 32k causal layer)
-template <> struct TileCfg<128> { static constexpr int BN = 32, OCC = 3, NBUF = 2; };
-template <> struct TileCfg<256> { static constexpr int BN = 32, OCC = 1, NBUF = 2; };
+template <> struct TileCfg<64> { static constexpr int BN = 64, OCC = 4, NBUF = 2; };    // 116 VGPRs, 32 KiB LDS
+template <> struct TileCfg<128> { static constexpr int BN = 32, OCC = 3, NBUF = 2; };   // 148 VGPRs, 32 KiB LDS
+template <> struct TileCfg<256> { static constexpr int BN = 32, OCC = 2, NBUF = 2; };   // 248 VGPRs, 64 KiB LDS
 
 // Row of the 32-key block that MFMA A-row r reads: bits 2 and 3 of r swapped.
 __device__ __forceinline__ int key_row(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
