@@ -48,11 +48,20 @@ constexpr float kTau = 8.0f;
 // Buffer resource word 3 for raw 32-bit accesses (bounds-checked against num_records, zero past the end).
 constexpr int kBufferFlags = 0x00020000;
 
-// Per head size: keys per step (BN), workgroups per CU (occupancy; registers and LDS both fit it) and K/V buffers.
+// Per head size: keys per step (BN), waves per SIMD (occupancy; registers and LDS both fit it) and K/V buffers.
+// D=64: 4-wave workgroups, 116 VGPRs, 32 KiB LDS, four per CU. D=128: one 12-wave workgroup per CU (three waves
+// per SIMD) sharing one 64-key K/V stream, 164 VGPRs, 64 KiB LDS. D=256: one 8-wave workgroup per CU, 248 VGPRs,
+// 64 KiB LDS.
+#ifndef KA_OCC128
+#define KA_OCC128 3
+#endif
+#ifndef KA_OCC256
+#define KA_OCC256 2
+#endif
 template <int D> struct TileCfg;
-template <> struct TileCfg<64> { static constexpr int BN = 64, OCC = 4, NBUF = 2; };    // 116 VGPRs, 32 KiB LDS
-template <> struct TileCfg<128> { static constexpr int BN = 32, OCC = 3, NBUF = 2; };   // 148 VGPRs, 32 KiB LDS
-template <> struct TileCfg<256> { static constexpr int BN = 32, OCC = 2, NBUF = 2; };   // 248 VGPRs, 64 KiB LDS
+template <> struct TileCfg<64> { static constexpr int BN = tile_keys(64), OCC = 4, NBUF = 2; };
+template <> struct TileCfg<128> { static constexpr int BN = tile_keys(128), OCC = KA_OCC128, NBUF = 2; };
+template <> struct TileCfg<256> { static constexpr int BN = tile_keys(256), OCC = KA_OCC256, NBUF = 2; };
 
 // Row of the 32-key block that MFMA A-row r reads: bits 2 and 3 of r swapped.
 __device__ __forceinline__ int key_row(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
@@ -119,26 +128,29 @@ __device__ __forceinline__ void dma_16b(const uint16_t* base, int bytes, KA_LDS 
 }
 
 template <int D>
-__global__ __launch_bounds__(kThreads, TileCfg<D>::OCC) void attn_fwd_kernel(Params p) {
+__global__ __launch_bounds__(64 * tile_waves(D), TileCfg<D>::OCC) void attn_fwd_kernel(Params p) {
+  constexpr int W = tile_waves(D);  // waves of the workgroup
   constexpr int BN = TileCfg<D>::BN;
   constexpr int DC = D / 16;       // 16-wide head-dim chunks of the QK^T contraction
   constexpr int DB = D / 32;       // 32-row head-dim blocks of O^T
   constexpr int KB = BN / 32;      // 32-key blocks of S^T
   constexpr int KC = BN / 16;      // 16-key chunks of the PV contraction
   constexpr int TILE = BN * D * 2;  // bytes of one K or V tile
-  constexpr int INSTS = TILE / 1024 / kWaves;  // DMA instructions per wave per tile
-  static_assert(INSTS >= 1, "a tile must give every wave at least one DMA instruction");
+  constexpr int BLKS = TILE / 1024;               // 1 KiB DMA instructions per K or V tile
+  constexpr int INSTS = (BLKS + W - 1) / W;       // per wave (the last waves may issue fewer)
+  static_assert(BLKS >= 1, "a tile holds at least one DMA instruction");
 
   // separate arrays per buffer: the compiler then sees that a step's copy never writes the tiles it reads
   constexpr int NBUF = TileCfg<D>::NBUF;
   static_assert(NBUF == 2 || NBUF == 3, "two or three K/V buffers");
+  static_assert(NBUF == 2 || BLKS % W == 0, "partial vmcnt waits need every wave to issue the same copies");
   __shared__ __attribute__((aligned(1024))) char k_lds0[TILE];
   __shared__ __attribute__((aligned(1024))) char k_lds1[TILE];
   __shared__ __attribute__((aligned(1024))) char k_lds2[NBUF > 2 ? TILE : 16];
   __shared__ __attribute__((aligned(1024))) char v_lds0[TILE];
   __shared__ __attribute__((aligned(1024))) char v_lds1[TILE];
   __shared__ __attribute__((aligned(1024))) char v_lds2[NBUF > 2 ? TILE : 16];
-  __shared__ int red[2][kWaves];
+  __shared__ int red[2][W];
 
   const int n_tiles = p.plan[0];
   const int item = blockIdx.x / p.n_hg;
@@ -219,7 +231,7 @@ __global__ __launch_bounds__(kThreads, TileCfg<D>::OCC) void attn_fwd_kernel(Par
   __syncthreads();
   int klo = INT32_MAX, khi = INT32_MIN;
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
+  for (int w = 0; w < W; ++w) {
     klo = min(klo, red[0][w]);
     khi = max(khi, red[1][w]);
   }
@@ -246,13 +258,17 @@ __global__ __launch_bounds__(kThreads, TileCfg<D>::OCC) void attn_fwd_kernel(Par
     const int rows = min(lk - j0, BN);
     const uint16_t* ks = kbase + (int64_t)j0 * p.sk_t;
 #pragma unroll
-    for (int r = 0; r < INSTS; ++r) dma_16b(ks, rows * (int)p.sk_t * 2, kt + (wave * INSTS + r) * 1024, k_voff[r]);
+    for (int r = 0; r < INSTS; ++r)
+      if (BLKS % W == 0 || wave * INSTS + r < BLKS)
+        dma_16b(ks, rows * (int)p.sk_t * 2, kt + (wave * INSTS + r) * 1024, k_voff[r]);
   };
   auto copy_v = [&](int j0, KA_LDS char* vt) {
     const int rows = min(lk - j0, BN);
     const uint16_t* vs = vbase + (int64_t)j0 * p.sv_t;
 #pragma unroll
-    for (int r = 0; r < INSTS; ++r) dma_16b(vs, rows * (int)p.sv_t * 2, vt + (wave * INSTS + r) * 1024, v_voff[r]);
+    for (int r = 0; r < INSTS; ++r)
+      if (BLKS % W == 0 || wave * INSTS + r < BLKS)
+        dma_16b(vs, rows * (int)p.sv_t * 2, vt + (wave * INSTS + r) * 1024, v_voff[r]);
   };
   auto copy_step = [&](int j0, KA_LDS char* kt, KA_LDS char* vt) {
     copy_k(j0, kt);
@@ -507,7 +523,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* __res
 
 template <int D>
 static hipError_t launch_attn(const Params& p, int64_t grid, hipStream_t stream) {
-  hipLaunchKernelGGL((attn_fwd_kernel<D>), dim3((unsigned)grid), dim3(kThreads), 0, stream, p);
+  hipLaunchKernelGGL((attn_fwd_kernel<D>), dim3((unsigned)grid), dim3(64 * tile_waves(D)), 0, stream, p);
   return hipGetLastError();
 }
 

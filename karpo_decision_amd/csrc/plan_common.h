@@ -15,8 +15,18 @@
 
 namespace karpo {
 
-constexpr int kWaves = 4;            // waves per workgroup
-constexpr int kThreads = 64 * kWaves;
+#ifndef KA_W128
+#define KA_W128 12
+#endif
+#ifndef KA_W256
+#define KA_W256 8
+#endif
+#ifndef KA_BN128
+#define KA_BN128 64
+#endif
+// Waves per workgroup (each holds 32 query vectors of the tile) and keys per step, per head size.
+KA_HD constexpr int tile_waves(int head_dim) { return head_dim == 128 ? KA_W128 : head_dim == 256 ? KA_W256 : 4; }
+KA_HD constexpr int tile_keys(int head_dim) { return head_dim == 128 ? KA_BN128 : head_dim == 256 ? 32 : 64; }
 constexpr int kPlanHeader = 4;       // int32 header of a plan: tiles, rows per tile, keys per step, heads per item
 constexpr int kCostBuckets = 2048;   // device planner's cost histogram (costs clamp to the last bucket)
 
@@ -32,8 +42,8 @@ KA_HD inline bool head_dim_supported(int d) { return d == 64 || d == 128 || d ==
 
 KA_HD inline Geometry geometry(int heads, int kv_heads, int head_dim) {
   Geometry g;
-  g.vectors = 32 * kWaves;
-  g.bn = head_dim <= 64 ? 64 : 32;  // keys per step of the kernel for this head size
+  g.vectors = 32 * tile_waves(head_dim);
+  g.bn = tile_keys(head_dim);
   int group = heads / kv_heads;
   g.ng = (g.vectors % group == 0) ? group : 1;
   g.rows = g.vectors / g.ng;

@@ -221,6 +221,22 @@ def test_large_logits_match_float32_math(gpu, heads, kv_heads, head):
     assert_close(got, want, "large logits")
 
 
+@pytest.mark.parametrize("heads,kv_heads,head", [(12, 4, 128), (10, 2, 128), (6, 2, 256), (12, 4, 64), (5, 5, 128)])
+def test_gqa_groups_that_do_and_do_not_divide_a_tile(gpu, heads, kv_heads, head):
+    """A group of 3 divides a 384-vector tile (its heads share one K/V stream), a group of 5 does not (one query head
+    per work item); both must read K/V head h // G."""
+    torch.manual_seed(10)
+    q_cu = [0, 333, 1000, 1001]
+    q = torch.randn(1001, heads, head, device=gpu).bfloat16()
+    k = torch.randn(1001, kv_heads, head, device=gpu).bfloat16()
+    v = torch.randn(1001, kv_heads, head, device=gpu).bfloat16()
+    cu = torch.tensor(q_cu, dtype=torch.int32, device=gpu)
+    with torch.inference_mode():
+        got = ops.run(q, k, v, cu, cu, 667, 1 / math.sqrt(head), -1, 0)
+    want = oa.packed_attention(q.cpu(), k.cpu(), v.cpu(), q_cu, q_cu, 1 / math.sqrt(head), -1, 0)
+    assert_close(got, want, f"gqa {heads}/{kv_heads}/{head}")
+
+
 def test_negative_and_zero_scale(gpu):
     torch.manual_seed(5)
     q = torch.randn(200, 8, 64, device=gpu).bfloat16()

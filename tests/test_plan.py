@@ -46,7 +46,7 @@ def host_plan(q_cu, k_cu, heads, kv_heads, head_dim, left, right):
     return list(buf[:4]), [(buf[4 + 2 * i], buf[5 + 2 * i]) for i in range(tiles)]
 
 
-GEOMETRIES = [(8, 2, 64), (16, 8, 128), (32, 16, 128), (16, 8, 256), (12, 4, 128), (4, 4, 64)]
+GEOMETRIES = [(8, 2, 64), (16, 8, 128), (32, 16, 128), (16, 8, 256), (12, 4, 128), (10, 2, 128), (4, 4, 64)]
 
 
 @settings(max_examples=60, deadline=None)
@@ -70,11 +70,13 @@ def test_host_plan_matches_brute_force(q_lens, extra, geom, left, right):
 
 
 def test_tile_geometry():
-    # a tile holds 128 query vectors: the GQA group's heads share it when they divide it
-    assert _lib.tile_shape(32, 16, 128) == (64, 32, 2)
+    # a tile holds 32 query vectors per wave (12 waves at head_dim 128, 8 at 256, 4 at 64); the GQA group's heads
+    # share it when they divide it
+    assert _lib.tile_shape(32, 16, 128) == (192, 64, 2)
     assert _lib.tile_shape(8, 2, 64) == (32, 64, 4)
-    assert _lib.tile_shape(16, 8, 256) == (64, 32, 2)
-    assert _lib.tile_shape(12, 4, 128) == (128, 32, 1)  # group of 3: one head per item
+    assert _lib.tile_shape(16, 8, 256) == (128, 32, 2)
+    assert _lib.tile_shape(12, 4, 128) == (128, 64, 3)  # a group of 3 divides 384 vectors
+    assert _lib.tile_shape(10, 2, 128) == (384, 64, 1)  # a group of 5 does not: one head per item
 
 
 def test_plan_refuses_bad_bounds_and_small_buffers():
@@ -144,7 +146,7 @@ def test_workspace_and_capacity():
 
 def test_python_plan_object():
     plan = ops.make_plan([0, 100, 400], [0, 100, 400], 32, 16, 128, -1, 0, device="cpu")
-    assert plan.tiles == 2 + 5 and plan.rows_per_tile == 64
+    assert plan.tiles == 1 + 2 and plan.rows_per_tile == 192
     assert plan.tensor.dtype.is_signed and plan.tensor.numel() == 4 + 2 * plan.tiles
 
 
