@@ -72,31 +72,45 @@ typedef struct KarpoAttnArgs {
   const int32_t* spans;  /* device, [n_spans][2] half-open query-row ranges [s, e) in pack rows, or NULL */
   int32_t n_spans;       /* spans sorted by start, non-overlapping, each inside one sequence */
   const int32_t* plan;   /* device plan from karpo_attn_plan (copied to the device), or NULL: plan on the device */
-  void* workspace;       /* device scratch of karpo_attn_workspace_bytes bytes (unused when plan != NULL) */
+  void* workspace;       /* device scratch of karpo_attn_workspace_bytes bytes: the device plan and the partial
+                            results of split tiles */
   size_t workspace_bytes;
+  int32_t plan_unsplit;  /* nonzero when args->plan splits no tile (its plan[4] == 0): the merge kernel is not
+                            launched. 0 (always safe) when unknown. Ignored without a plan. */
 } KarpoAttnArgs;
 
-/* Bytes of device workspace karpo_attn_fwd needs for these arguments when args->plan is NULL
- * (reads only sizes: heads, kv_heads, head_dim, n_seq, total_q, max_q). */
+/* Bytes of device workspace karpo_attn_fwd needs for these arguments (reads only sizes: heads, kv_heads, head_dim,
+ * n_seq, total_q, max_q). It holds the device plan (when args->plan is NULL) and the fp32 partial results of tiles
+ * the plan splits over their keys; only a call with a host plan marked plan_unsplit may pass none. Calls that
+ * overlap on one device need separate workspaces. */
 int karpo_attn_workspace_bytes(const KarpoAttnArgs* args, size_t* bytes);
 
 /* Int32 entries a plan buffer for these arguments holds at most (the capacity to give karpo_attn_plan). */
 int karpo_attn_plan_capacity(const KarpoAttnArgs* args, int64_t* entries);
 
-/* The forward pass on `stream` (a hipStream_t; NULL is the null stream). Plans on the device first unless
- * args->plan is set. Replaces triton_attention.attend's launch (triton_attention.py:103-109); the caller owns o. */
+/* The forward pass on `stream` (a hipStream_t; NULL is the null stream): the device planner unless args->plan is set,
+ * the attention kernel, and the merge kernel that combines the parts of split tiles. Replaces
+ * triton_attention.attend's launch (triton_attention.py:103-109); the caller owns o. */
 int karpo_attn_fwd(const KarpoAttnArgs* args, void* stream);
 
-/* The work list on the host from host copies of the bounds, in the layout the kernel reads:
- *   plan[0] = tiles, plan[1] = query rows per tile, plan[2] = keys per step, plan[3] = heads per work item,
- *   then per tile (segment, tile index), longest first (ties in segment, tile order).
- * Replaces the host-side bound building of block_plan (families/gemma/packed.py:103-151); like it, it runs once per
- * pack and its result is reused by every layer of the same geometry. Reads heads, kv_heads, head_dim, window_*. */
+/* The work list on the host from host copies of the bounds, in the layout the kernels read:
+ *   plan[0] = work items, plan[1] = query rows per tile, plan[2] = keys per step, plan[3] = heads per work item,
+ *   plan[4] = split tiles, plan[5] = waves per workgroup, plan[6] = offset of the first item, plan[7] = partial
+ *   slots used;
+ *   at plan[8]: per split tile (segment, tile, parts, first partial slot), in segment, tile order;
+ *   at plan[plan[6]]: per item (segment, tile, part | parts << 16, first partial slot or -1), longest first (ties in
+ *   segment, tile, part order).
+ * A tile visits the key steps its queries can see; one whose steps exceed the pack's per-workgroup share is split
+ * into parts over those steps (the policy depends only on the bounds and the tile shape). Replaces the host-side
+ * bound building of block_plan (families/gemma/packed.py:103-151); like it, it runs once per pack and its result is
+ * reused by every layer of the same geometry. Reads heads, kv_heads, head_dim, max_q, window_*; a plan is only valid
+ * for karpo_attn_fwd calls with the same values (max_q selects the tile shape). */
 int karpo_attn_plan(const KarpoAttnArgs* args, const int32_t* q_cu_host, const int32_t* k_cu_host, int32_t n_seq,
                     int32_t* plan, int64_t capacity);
 
-/* Query rows per tile and keys per step the kernel uses for these heads / head size. */
-int karpo_attn_tile_shape(int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t* rows_per_tile,
+/* Query rows per tile, keys per step and query heads per work item the kernel uses for these heads / head size and
+ * the longest query run max_q (packs whose sequences fit one wave's 32 query vectors take one-wave tiles). */
+int karpo_attn_tile_shape(int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t max_q, int32_t* rows_per_tile,
                           int32_t* keys_per_step, int32_t* heads_per_item);
 
 /* A static message for a status code. */

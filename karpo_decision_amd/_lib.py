@@ -1,4 +1,4 @@
-"""ctypes binding of ``libkarpo_attn.so`` (``include/karpo_attn.h``). The library is the only compute path: if it is
+"""ctypes binding of ``libkarpo_attn.so`` (``include/karpo_attn.h``, version 2). The library is the only compute path: if it is
 missing this module raises, it never falls back to another implementation."""
 
 from __future__ import annotations
@@ -33,6 +33,7 @@ class KarpoAttnArgs(ctypes.Structure):
         ("window_left", ctypes.c_int32), ("window_right", ctypes.c_int32),
         ("spans", ctypes.c_void_p), ("n_spans", ctypes.c_int32),
         ("plan", ctypes.c_void_p), ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+        ("plan_unsplit", ctypes.c_int32),
     ]
 
 
@@ -60,8 +61,8 @@ def load() -> ctypes.CDLL:
         lib.karpo_attn_plan_capacity.restype = ctypes.c_int
         lib.karpo_attn_workspace_bytes.argtypes = [P(KarpoAttnArgs), P(ctypes.c_size_t)]
         lib.karpo_attn_workspace_bytes.restype = ctypes.c_int
-        lib.karpo_attn_tile_shape.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, P(ctypes.c_int32),
-                                              P(ctypes.c_int32), P(ctypes.c_int32)]
+        lib.karpo_attn_tile_shape.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                              P(ctypes.c_int32), P(ctypes.c_int32), P(ctypes.c_int32)]
         lib.karpo_attn_tile_shape.restype = ctypes.c_int
         lib.karpo_attn_strerror.argtypes = [ctypes.c_int]
         lib.karpo_attn_strerror.restype = ctypes.c_char_p
@@ -83,9 +84,14 @@ def check(status: int, what: str) -> None:
     raise (ValueError if status in VALUE_ERRORS else RuntimeError)(text)
 
 
-def tile_shape(heads: int, kv_heads: int, head_dim: int) -> tuple[int, int, int]:
-    """(query rows per tile, keys per step, query heads per work item)."""
+#: ``max_q`` of a prefill-sized pack (wide tiles whatever the head geometry).
+LONG = 1 << 30
+
+
+def tile_shape(heads: int, kv_heads: int, head_dim: int, max_q: int = LONG) -> tuple[int, int, int]:
+    """(query rows per tile, keys per step, query heads per work item) for packs whose longest query run is
+    ``max_q`` (one-wave tiles when every run fits one)."""
     rows, keys, per = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
-    check(load().karpo_attn_tile_shape(heads, kv_heads, head_dim, ctypes.byref(rows), ctypes.byref(keys),
+    check(load().karpo_attn_tile_shape(heads, kv_heads, head_dim, max_q, ctypes.byref(rows), ctypes.byref(keys),
                                        ctypes.byref(per)), "karpo_attn_tile_shape")
     return rows.value, keys.value, per.value

@@ -7,11 +7,12 @@
 // and denominator carry the same weights. Masks (causal / window / image span, varlen alignment of
 // tests/test_gemma_blocks.py:28-43) are evaluated per element only on key steps that cut through a wave's queries.
 //
-// Mapping onto a CU: two independent 4-wave workgroups per CU (two waves per SIMD). A wave's exponentials and row
-// reductions run on the VALU while the other workgroup's wave on the same SIMD keeps the matrix core busy, so no
-// in-wave software pipelining is needed. One work item = one query tile x one head group:
-//   * each wave holds 32 query vectors (position, head) of the tile in registers as MFMA B operands;
-//   * per step, BN keys of K and V are copied global -> LDS by the DMA path (global_load_lds, 16 B per lane),
+// Mapping onto a CU. One work item = one query tile x one head group, over all or one part of the tile's key steps:
+//   * each wave holds 32 query vectors (position, head) of the tile in registers as MFMA B operands; the waves of a
+//     workgroup share one K/V stream (wide tiles: 12 waves at head_dim 128, three per SIMD, so one wave's softmax
+//     VALU work runs beside another wave's MFMAs; 8 at 256; 4 at 64), or a workgroup is one wave (narrow tiles for
+//     decode-shaped packs, several workgroups per CU);
+//   * per step, BN keys of K and V are copied global -> LDS by the DMA path (buffer_load ... lds, 16 B per lane),
 //     double buffered, the next step's copy in flight while this step computes;
 //   * S^T = K Q^T on v_mfma_f32_32x32x16_bf16: a lane owns one query column, so the row max and sum are in-lane plus
 //     one v_permlane32_swap between the two half-waves;
@@ -22,7 +23,9 @@
 //     the 64 banks): K as [16-key block][16-byte chunk][16 keys], V as [4-key group][16-wide d block][4 keys][16 d];
 //     every per-step address is a lane base plus an immediate offset;
 //   * the running maximum is only raised when a step's maximum exceeds it by more than 2^8 (exact: the final
-//     division by l cancels any common factor), so O is rescaled on few steps.
+//     division by l cancels any common factor), so O is rescaled on few steps;
+//   * a part of a split tile stores its unnormalised fp32 O, running maximum m and sum l; merge_kernel combines the
+//     parts as O = sum_p 2^(m_p - M) O_p / sum_p 2^(m_p - M) l_p with M = max_p m_p.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -48,20 +51,21 @@ constexpr float kTau = 8.0f;
 // Buffer resource word 3 for raw 32-bit accesses (bounds-checked against num_records, zero past the end).
 constexpr int kBufferFlags = 0x00020000;
 
-// Per head size: keys per step (BN), waves per SIMD (occupancy; registers and LDS both fit it) and K/V buffers.
-// D=64: 4-wave workgroups, 116 VGPRs, 32 KiB LDS, four per CU. D=128: one 12-wave workgroup per CU (three waves
-// per SIMD) sharing one 64-key K/V stream, 164 VGPRs, 64 KiB LDS. D=256: one 8-wave workgroup per CU, 248 VGPRs,
-// 64 KiB LDS.
+// Per head size and tile shape: keys per step (BN) and waves per SIMD the registers are budgeted for (OCC).
+// Wide: D=64 4-wave workgroups, four per CU; D=128 one 12-wave workgroup per CU (three waves per SIMD) sharing one
+// 64-key K/V stream, 64 KiB LDS; D=256 one 8-wave workgroup per CU, 64 KiB LDS. Narrow: one wave per workgroup,
+// 32 KiB LDS (64 KiB at D=256), LDS-limited to five (two) per CU.
 #ifndef KA_OCC128
 #define KA_OCC128 3
 #endif
 #ifndef KA_OCC256
 #define KA_OCC256 2
 #endif
-template <int D> struct TileCfg;
-template <> struct TileCfg<64> { static constexpr int BN = tile_keys(64), OCC = 4, NBUF = 2; };
-template <> struct TileCfg<128> { static constexpr int BN = tile_keys(128), OCC = KA_OCC128, NBUF = 2; };
-template <> struct TileCfg<256> { static constexpr int BN = tile_keys(256), OCC = KA_OCC256, NBUF = 2; };
+template <int D, bool NARROW> struct TileCfg {
+  static constexpr int W = tile_waves(D, NARROW);
+  static constexpr int BN = tile_keys(D, NARROW);
+  static constexpr int OCC = NARROW ? 2 : D == 64 ? 4 : D == 128 ? KA_OCC128 : KA_OCC256;
+};
 
 // Row of the 32-key block that MFMA A-row r reads: bits 2 and 3 of r swapped.
 __device__ __forceinline__ int key_row(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
@@ -127,10 +131,10 @@ __device__ __forceinline__ void dma_16b(const uint16_t* base, int bytes, KA_LDS 
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (KA_LDS void*)lds, 16, voff, 0, 0, 0);
 }
 
-template <int D>
-__global__ __launch_bounds__(64 * tile_waves(D), TileCfg<D>::OCC) void attn_fwd_kernel(Params p) {
-  constexpr int W = tile_waves(D);  // waves of the workgroup
-  constexpr int BN = TileCfg<D>::BN;
+template <int D, bool NARROW>
+__global__ __launch_bounds__((64 * TileCfg<D, NARROW>::W), (TileCfg<D, NARROW>::OCC)) void attn_fwd_kernel(Params p) {
+  constexpr int W = TileCfg<D, NARROW>::W;  // waves of the workgroup
+  constexpr int BN = TileCfg<D, NARROW>::BN;
   constexpr int DC = D / 16;       // 16-wide head-dim chunks of the QK^T contraction
   constexpr int DB = D / 32;       // 32-row head-dim blocks of O^T
   constexpr int KB = BN / 32;      // 32-key blocks of S^T
@@ -141,23 +145,24 @@ __global__ __launch_bounds__(64 * tile_waves(D), TileCfg<D>::OCC) void attn_fwd_
   static_assert(BLKS >= 1, "a tile holds at least one DMA instruction");
 
   // separate arrays per buffer: the compiler then sees that a step's copy never writes the tiles it reads
-  constexpr int NBUF = TileCfg<D>::NBUF;
-  static_assert(NBUF == 2 || NBUF == 3, "two or three K/V buffers");
-  static_assert(NBUF == 2 || BLKS % W == 0, "partial vmcnt waits need every wave to issue the same copies");
   __shared__ __attribute__((aligned(1024))) char k_lds0[TILE];
   __shared__ __attribute__((aligned(1024))) char k_lds1[TILE];
-  __shared__ __attribute__((aligned(1024))) char k_lds2[NBUF > 2 ? TILE : 16];
   __shared__ __attribute__((aligned(1024))) char v_lds0[TILE];
   __shared__ __attribute__((aligned(1024))) char v_lds1[TILE];
-  __shared__ __attribute__((aligned(1024))) char v_lds2[NBUF > 2 ? TILE : 16];
-  __shared__ int red[2][W];
+  __shared__ int red[2][W];  // the workgroup's key envelope (unused, so not allocated, by one-wave workgroups)
 
-  const int n_tiles = p.plan[0];
+  // a plan made for another tile shape is not run (its rows stay unwritten)
+  if (p.plan[2] != BN || p.plan[5] != W) return;
+  const int n_items = p.plan[0];
   const int item = blockIdx.x / p.n_hg;
   const int hg = blockIdx.x - item * p.n_hg;
-  if (item >= n_tiles) return;
-  const int seg = p.plan[kPlanHeader + 2 * item];
-  const int tile = p.plan[kPlanHeader + 2 * item + 1];
+  if (item >= n_items) return;
+  const int32_t* entry = p.plan + p.plan[6] + kItemInts * item;
+  const int seg = entry[0];
+  const int tile = entry[1];
+  const int part = entry[2] & 0xffff, parts = entry[2] >> 16;
+  const int slot = entry[3];
+  if (parts > 1 && (slot < 0 || slot + part >= p.slots)) return;  // a partial slot outside the workspace
   const int rows_per_tile = p.plan[1];
   const int qa = p.q_cu[seg], lq = p.q_cu[seg + 1] - qa;
   const int ka = p.k_cu[seg], lk = p.k_cu[seg + 1] - ka;
@@ -212,9 +217,11 @@ __global__ __launch_bounds__(64 * tile_waves(D), TileCfg<D>::OCC) void attn_fwd_
   whi = __builtin_amdgcn_readfirstlane(wave_max(whi));
   wflo = __builtin_amdgcn_readfirstlane(wave_max(wflo));
   wfhi = __builtin_amdgcn_readfirstlane(wave_min(wfhi));
-  if (lane == 0) {
-    red[0][wave] = wlo;
-    red[1][wave] = whi;
+  if constexpr (W > 1) {
+    if (lane == 0) {
+      red[0][wave] = wlo;
+      red[1][wave] = whi;
+    }
   }
 
   bf16x8 qop[DC];
@@ -228,17 +235,24 @@ __global__ __launch_bounds__(64 * tile_waves(D), TileCfg<D>::OCC) void attn_fwd_
       qop[dc] = __builtin_bit_cast(bf16x8, x);
     }
   }
-  __syncthreads();
-  int klo = INT32_MAX, khi = INT32_MIN;
+  int klo = wlo, khi = whi;
+  if constexpr (W > 1) {
+    __syncthreads();
 #pragma unroll
-  for (int w = 0; w < W; ++w) {
-    klo = min(klo, red[0][w]);
-    khi = max(khi, red[1][w]);
+    for (int w = 0; w < W; ++w) {
+      klo = min(klo, red[0][w]);
+      khi = max(khi, red[1][w]);
+    }
+    klo = __builtin_amdgcn_readfirstlane(klo);
+    khi = __builtin_amdgcn_readfirstlane(khi);
   }
-  klo = __builtin_amdgcn_readfirstlane(klo);
-  khi = __builtin_amdgcn_readfirstlane(khi);
-  const int j_first = klo < khi ? (klo / BN) * BN : 0;
-  const int n_steps = klo < khi ? (khi - j_first + BN - 1) / BN : 0;
+  int j_first = klo < khi ? (klo / BN) * BN : 0;
+  int n_steps = klo < khi ? (khi - j_first + BN - 1) / BN : 0;
+  if (parts > 1) {  // this part's share of the envelope's steps (possibly none)
+    const int s0 = (int)((int64_t)part * n_steps / parts), s1 = (int)((int64_t)(part + 1) * n_steps / parts);
+    j_first += s0 * BN;
+    n_steps = s1 - s0;
+  }
 
   // ---- DMA: per instruction a lane's byte offset inside the step's rows (fixed for the kernel). Each step's rows
   // are one buffer resource starting at the step's first key row, sized to the rows that exist: reads past the
@@ -289,20 +303,17 @@ __global__ __launch_bounds__(64 * tile_waves(D), TileCfg<D>::OCC) void attn_fwd_
 
   KA_LDS char* const kt0 = (KA_LDS char*)k_lds0;
   KA_LDS char* const kt1 = (KA_LDS char*)k_lds1;
-  KA_LDS char* const kt2 = (KA_LDS char*)k_lds2;
   KA_LDS char* const vt0 = (KA_LDS char*)v_lds0;
   KA_LDS char* const vt1 = (KA_LDS char*)v_lds1;
-  KA_LDS char* const vt2 = (KA_LDS char*)v_lds2;
-  // prologue: the first NBUF - 1 steps in flight, wait for the first
+  // prologue: the first step in flight, wait for it
   if (n_steps > 0) copy_step(j_first, kt0, vt0);
-  if (NBUF > 2 && n_steps > 1) copy_step(j_first + BN, kt1, vt1);
-  if (NBUF > 2 && n_steps > 1) wait_vmcnt<2 * INSTS>(); else wait_vmcnt<0>();
+  wait_vmcnt<0>();
   __syncthreads();
 
-  // step s: copy step s + NBUF - 1 into (kn, vn) while computing on (kt, vt); then wait for step s + 1's copy
+  // step s: copy step s + 1 into (kn, vn) while computing on (kt, vt); then wait for that copy
   auto step = [&](int s, const KA_LDS char* kt, const KA_LDS char* vt, KA_LDS char* kn, KA_LDS char* vn) {
     const int j0 = j_first + s * BN;
-    if (s + NBUF - 1 < n_steps) copy_step(j0 + (NBUF - 1) * BN, kn, vn);
+    if (s + 1 < n_steps) copy_step(j0 + BN, kn, vn);
     if (j0 < whi && j0 + BN > wlo) {  // wave-uniform: some query of this wave sees a key of this step
       f32x16 st[KB];
 #pragma unroll
@@ -371,30 +382,35 @@ __global__ __launch_bounds__(64 * tile_waves(D), TileCfg<D>::OCC) void attn_fwd_
         }
       }
     }
-    // copies issued after step s + 1's: min(NBUF - 2, n_steps - 2 - s); only a full set may stay in flight
-    if (NBUF > 2 && n_steps - 2 - s >= NBUF - 2) wait_vmcnt<2 * INSTS * (NBUF - 2)>(); else wait_vmcnt<0>();
+    wait_vmcnt<0>();
     __syncthreads();
   };
   int s = 0;
-  if constexpr (NBUF == 2) {
-    for (; s + 1 < n_steps; s += 2) {
-      step(s, kt0, vt0, kt1, vt1);
-      step(s + 1, kt1, vt1, kt0, vt0);
-    }
-    if (s < n_steps) step(s, kt0, vt0, kt1, vt1);
-  } else {
-    for (; s + 2 < n_steps; s += 3) {
-      step(s, kt0, vt0, kt2, vt2);
-      step(s + 1, kt1, vt1, kt0, vt0);
-      step(s + 2, kt2, vt2, kt1, vt1);
-    }
-    if (s < n_steps) step(s, kt0, vt0, kt2, vt2);
-    if (s + 1 < n_steps) step(s + 1, kt1, vt1, kt0, vt0);
+  for (; s + 1 < n_steps; s += 2) {
+    step(s, kt0, vt0, kt1, vt1);
+    step(s + 1, kt1, vt1, kt0, vt0);
   }
+  if (s < n_steps) step(s, kt0, vt0, kt1, vt1);
 
-
-  // ---- normalise and store: lane (col, half) holds d = db*32 + (j/4)*8 + half*4 + j%4 of its query
+  // ---- store: lane (col, half) holds d = db*32 + (j/4)*8 + half*4 + j%4 of its query vector
   const float lt = half_swap_sum(l);
+  if (parts > 1) {  // one part of a split tile: unnormalised fp32 O, m and l for merge_kernel
+    constexpr int V = 32 * W;
+    float* base = p.partial + ((int64_t)(slot + part) * p.n_hg + hg) * (int64_t)V * (D + 2);
+    float* op = base + (int64_t)vec * D + half * 4;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        float4 x = {acc[db][g4 * 4], acc[db][g4 * 4 + 1], acc[db][g4 * 4 + 2], acc[db][g4 * 4 + 3]};
+        *(float4*)(op + db * 32 + g4 * 8) = x;
+      }
+    if (half == 0) {
+      base[V * D + vec] = m;
+      base[V * D + V + vec] = lt;
+    }
+    return;
+  }
   const float inv = lt > 0.f ? 1.f / lt : 0.f;
   if (valid) {
     uint16_t* op = p.o + (int64_t)(qa + pos) * p.so_t + (int64_t)head * p.so_h + half * 4;
@@ -412,6 +428,61 @@ __global__ __launch_bounds__(64 * tile_waves(D), TileCfg<D>::OCC) void attn_fwd_
         *(u32x2*)(op + db * 32 + g4 * 8) = w;
       }
     }
+  }
+}
+
+// ---- merge: the parts of split tiles. Thread per (split tile, head group, query vector, 4 head-dim elements), in a
+// grid-stride loop over a fixed grid, so every load of a thread is independent and the launch costs little when the
+// plan splits nothing. The parts' running maxima go on a common M: O = sum_p 2^(m_p - M) O_p / sum_p 2^(m_p - M) l_p
+// (0 when no part saw a key, as an unsplit tile writes).
+constexpr int kMergeThreads = 256;
+constexpr int kMergeBlocks = 1024;
+
+template <int D, int W>
+__global__ __launch_bounds__(kMergeThreads) void merge_kernel(Params p) {
+  constexpr int V = 32 * W, C4 = D / 4;
+  if (p.plan[5] != W) return;
+  const int64_t units = (int64_t)p.plan[4] * p.n_hg * V * C4;
+  const int rows_per_tile = p.plan[1];
+  const int64_t stride = (int64_t)p.n_hg * V * (D + 2);  // floats between consecutive slots
+  for (int64_t idx = (int64_t)blockIdx.x * kMergeThreads + threadIdx.x; idx < units;
+       idx += (int64_t)gridDim.x * kMergeThreads) {
+    const int d = (int)(idx % C4) * 4;
+    const int vec = (int)((idx / C4) % V);
+    const int64_t mh = idx / ((int64_t)C4 * V);
+    const int merge = (int)(mh / p.n_hg), hg = (int)(mh - (int64_t)merge * p.n_hg);
+    const int32_t* e = p.plan + kPlanHeader + kMergeInts * merge;
+    const int seg = e[0], tile = e[1], parts = e[2], slot = e[3];
+    if (slot < 0 || parts < 2 || slot + parts > p.slots) continue;
+    const int off = vec / p.ng;
+    const int pos = tile * rows_per_tile + off;
+    const int qa = p.q_cu[seg], lq = p.q_cu[seg + 1] - qa;
+    if (pos >= lq) continue;
+    const int head = hg * p.ng + (vec - off * p.ng);
+    const float* first = p.partial + ((int64_t)slot * p.n_hg + hg) * (int64_t)V * (D + 2);
+    float mx = -INFINITY;
+    for (int q = 0; q < parts; ++q) mx = fmaxf(mx, first[q * stride + V * D + vec]);
+    float4 num = {0.f, 0.f, 0.f, 0.f};
+    float den = 0.f;
+    if (mx != -INFINITY) {
+      for (int q = 0; q < parts; ++q) {
+        const float* b = first + q * stride;
+        const float w = __builtin_amdgcn_exp2f(b[V * D + vec] - mx);
+        const float4 x = *(const float4*)(b + (int64_t)vec * D + d);
+        num.x += w * x.x;
+        num.y += w * x.y;
+        num.z += w * x.z;
+        num.w += w * x.w;
+        den += w * b[V * D + V + vec];
+      }
+    }
+    const float inv = den > 0.f ? 1.f / den : 0.f;
+    const __bf16 r0 = (__bf16)(num.x * inv), r1 = (__bf16)(num.y * inv), r2 = (__bf16)(num.z * inv),
+                 r3 = (__bf16)(num.w * inv);
+    u32x2 w;
+    w[0] = (unsigned)__builtin_bit_cast(uint16_t, r0) | ((unsigned)__builtin_bit_cast(uint16_t, r1) << 16);
+    w[1] = (unsigned)__builtin_bit_cast(uint16_t, r2) | ((unsigned)__builtin_bit_cast(uint16_t, r3) << 16);
+    *(u32x2*)(p.o + (int64_t)(qa + pos) * p.so_t + (int64_t)head * p.so_h + d) = w;
   }
 }
 
@@ -445,46 +516,78 @@ __device__ int block_exclusive_scan(int x, int* total, int* scratch /* >= kPlanT
   return ex;
 }
 
+__device__ int64_t block_sum64(int64_t x, int64_t* scratch /* >= kPlanThreads/64 */) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+  if (lane == 0) scratch[wave] = x;
+  __syncthreads();
+  int64_t t = 0;
+#pragma unroll
+  for (int w = 0; w < kPlanThreads / 64; ++w) t += scratch[w];
+  __syncthreads();
+  return t;
+}
+
+// The plan of karpo_attn.h from the device bounds, in three passes over the tiles: the pack's workgroup-steps (which
+// set the split length), a histogram of part costs, and the scatter (descending cost order; split tiles' slots and
+// merge entries in tile order). The host planner (plan.cpp) lists the same items; among equal costs the order here
+// depends on atomics.
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* __restrict__ q_cu,
-                                                            const int32_t* __restrict__ k_cu, int n_seq, int rows,
-                                                            int bn, int ng, int left, int right,
-                                                            int32_t* __restrict__ plan, int capacity,
-                                                            int32_t* __restrict__ tile_base) {
+                                                            const int32_t* __restrict__ k_cu, int n_seq,
+                                                            Geometry g, int left, int right,
+                                                            int32_t* __restrict__ plan, int tiles_cap, int merges_cap,
+                                                            int items_cap, int32_t* __restrict__ tile_base) {
   __shared__ int hist[kCostBuckets];
   __shared__ int scratch[kPlanThreads / 64 + 1];
+  __shared__ int64_t scratch64[kPlanThreads / 64];
   const int tid = threadIdx.x;
   int carry = 0;
   for (int base = 0; base < n_seq; base += kPlanThreads) {
     const int i = base + tid;
-    const int nt = i < n_seq ? (int)tiles_of(q_cu[i + 1] - q_cu[i], rows) : 0;
+    const int nt = i < n_seq ? (int)tiles_of(q_cu[i + 1] - q_cu[i], g.rows) : 0;
     int total;
     const int ex = block_exclusive_scan(nt, &total, scratch);
     if (i < n_seq) tile_base[i] = carry + ex;
     carry += total;
   }
   if (tid == 0) tile_base[n_seq] = carry;
-  const int n_tiles = min(carry, capacity);
+  const int n_tiles = min(carry, tiles_cap);
   for (int b = tid; b < kCostBuckets; b += kPlanThreads) hist[b] = 0;
   __syncthreads();
 
-  auto locate = [&](int f, int* seg, int* cost) {
+  // tile f: its segment, index in the segment and key steps
+  auto locate = [&](int f, int* seg, int* t) -> int64_t {
     int l0 = 0, l1 = n_seq;  // last segment whose first tile is at or before f
     while (l1 - l0 > 1) {
       const int mid = (l0 + l1) >> 1;
       if (tile_base[mid] <= f) l0 = mid; else l1 = mid;
     }
-    const int t = f - tile_base[l0];
-    const int lq = q_cu[l0 + 1] - q_cu[l0], lk = k_cu[l0 + 1] - k_cu[l0];
     *seg = l0;
-    *cost = min(tile_cost(lq, lk, t, rows, bn, left, right), kCostBuckets - 1);
-    return t;
+    *t = f - tile_base[l0];
+    const int lq = q_cu[l0 + 1] - q_cu[l0], lk = k_cu[l0 + 1] - k_cu[l0];
+    return tile_steps(lq, lk, *t, g.rows, g.bn, left, right);
   };
+  int64_t mine = 0;
   for (int f = tid; f < n_tiles; f += kPlanThreads) {
-    int seg, cost;
-    locate(f, &seg, &cost);
-    atomicAdd(&hist[cost], 1);
+    int seg, t;
+    mine += locate(f, &seg, &t);
   }
-  __syncthreads();
+  const int64_t tau = split_tau(block_sum64(mine, scratch64) * g.n_hg, g.conc);
+
+  int64_t counts = 0;  // split tiles (high 32 bits) and items (low) of this thread's tiles
+  for (int f = tid; f < n_tiles; f += kPlanThreads) {
+    int seg, t;
+    const int64_t steps = locate(f, &seg, &t);
+    const int parts = split_parts(steps, tau);
+    atomicAdd(&hist[part_cost(steps, parts)], parts);
+    counts += (parts > 1 ? (int64_t)1 << 32 : 0) + parts;
+  }
+  const int64_t both = block_sum64(counts, scratch64);
+  // within the capacities by the split policy's bound; a plan that would not fit lists no items (never written)
+  const int n_merges = (int)(both >> 32), n_items = (int)(both & 0xffffffff);
+  const bool fits = n_merges <= merges_cap && n_items <= items_cap;
+  const int first = kPlanHeader + kMergeInts * min(n_merges, merges_cap);
   // descending exclusive scan: bucket b starts after every item of higher cost
   {
     constexpr int per = kCostBuckets / kPlanThreads;
@@ -503,44 +606,83 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* __res
     }
   }
   __syncthreads();
-  for (int f = tid; f < n_tiles; f += kPlanThreads) {
-    int seg, cost;
-    const int t = locate(f, &seg, &cost);
-    const int at = atomicAdd(&hist[cost], 1);
-    plan[kPlanHeader + 2 * at] = seg;
-    plan[kPlanHeader + 2 * at + 1] = t;
+  int slot_carry = 0, merge_carry = 0;
+  for (int base = 0; base < n_tiles; base += kPlanThreads) {
+    const int f = base + tid;
+    int seg = 0, t = 0, parts = 0;
+    int64_t steps = 0;
+    if (f < n_tiles) {
+      steps = locate(f, &seg, &t);
+      parts = split_parts(steps, tau);
+    }
+    const bool split = parts > 1;
+    int slots_total, merges_total;
+    const int slot = slot_carry + block_exclusive_scan(split ? parts : 0, &slots_total, scratch);
+    const int merge = merge_carry + block_exclusive_scan(split ? 1 : 0, &merges_total, scratch);
+    slot_carry += slots_total;
+    merge_carry += merges_total;
+    if (f >= n_tiles || !fits) continue;
+    if (split) {
+      int32_t* m = plan + kPlanHeader + kMergeInts * merge;
+      m[0] = seg;
+      m[1] = t;
+      m[2] = parts;
+      m[3] = slot;
+    }
+    const int at = atomicAdd(&hist[part_cost(steps, parts)], parts);
+    for (int q = 0; q < parts; ++q) {
+      int32_t* e = plan + first + kItemInts * (at + q);
+      e[0] = seg;
+      e[1] = t;
+      e[2] = q | (parts << 16);
+      e[3] = split ? slot : -1;
+    }
   }
   if (tid == 0) {
-    plan[0] = n_tiles;
-    plan[1] = rows;
-    plan[2] = bn;
-    plan[3] = ng;
+    plan[0] = fits ? n_items : 0;
+    plan[1] = g.rows;
+    plan[2] = g.bn;
+    plan[3] = g.ng;
+    plan[4] = fits ? n_merges : 0;
+    plan[5] = g.waves;
+    plan[6] = first;
+    plan[7] = slot_carry;
   }
 }
 
 // ---- launch
 
-
-template <int D>
-static hipError_t launch_attn(const Params& p, int64_t grid, hipStream_t stream) {
-  hipLaunchKernelGGL((attn_fwd_kernel<D>), dim3((unsigned)grid), dim3(64 * tile_waves(D)), 0, stream, p);
+template <int D, bool NARROW>
+static hipError_t launch_attn(const Params& p, int64_t items, int64_t merges, int n_hg, hipStream_t stream) {
+  hipLaunchKernelGGL((attn_fwd_kernel<D, NARROW>), dim3((unsigned)(items * n_hg)),
+                     dim3(64 * TileCfg<D, NARROW>::W), 0, stream, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || merges <= 0) return e;
+  constexpr int64_t per_merge = (int64_t)32 * TileCfg<D, NARROW>::W * (D / 4);  // threads of one head group
+  const int64_t blocks = (merges * n_hg * per_merge + kMergeThreads - 1) / kMergeThreads;
+  hipLaunchKernelGGL((merge_kernel<D, TileCfg<D, NARROW>::W>), dim3((unsigned)(blocks < kMergeBlocks ? blocks : kMergeBlocks)),
+                     dim3(kMergeThreads), 0, stream, p);
   return hipGetLastError();
 }
 
-hipError_t launch_forward(const Params& p, int head_dim, int64_t grid, hipStream_t stream) {
-  if (grid <= 0) return hipSuccess;
-  switch (head_dim) {
-    case 64: return launch_attn<64>(p, grid, stream);
-    case 128: return launch_attn<128>(p, grid, stream);
-    case 256: return launch_attn<256>(p, grid, stream);
+hipError_t launch_forward(const Params& p, int head_dim, const Geometry& g, int64_t items, int64_t merges,
+                          hipStream_t stream) {
+  if (items <= 0) return hipSuccess;
+  switch (head_dim * 2 + (g.narrow ? 1 : 0)) {
+    case 128: return launch_attn<64, false>(p, items, merges, g.n_hg, stream);
+    case 129: return launch_attn<64, true>(p, items, merges, g.n_hg, stream);
+    case 256: return launch_attn<128, false>(p, items, merges, g.n_hg, stream);
+    case 257: return launch_attn<128, true>(p, items, merges, g.n_hg, stream);
+    case 512: return launch_attn<256, false>(p, items, merges, g.n_hg, stream);
+    case 513: return launch_attn<256, true>(p, items, merges, g.n_hg, stream);
     default: return hipErrorInvalidValue;
   }
 }
 
 hipError_t launch_plan(const int32_t* q_cu, const int32_t* k_cu, int n_seq, const Geometry& g, int left, int right,
-                       int32_t* plan, int capacity, int32_t* tile_base, hipStream_t stream) {
-  hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, q_cu, k_cu, n_seq, g.rows, g.bn, g.ng, left,
-                     right, plan, capacity, tile_base);
+                       int32_t* plan, int tiles, int merges, int items, int32_t* tile_base, hipStream_t stream) {
+  hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, q_cu, k_cu, n_seq, g, left, right, plan,
+                     tiles, merges, items, tile_base);
   return hipGetLastError();
 }
 

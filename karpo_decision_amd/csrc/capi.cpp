@@ -33,11 +33,30 @@ int64_t tile_capacity(const KarpoAttnArgs* a, const Geometry& g) {
   return by_rows < by_max ? by_rows : by_max;
 }
 
+// Sizes of one call's plan and workspace. Items: every unsplit tile once plus the parts of split tiles (fewer than
+// split_slots); split tiles: fewer than half the slots.
+struct Sizes {
+  int64_t tiles, items, merges, plan_entries, partial_offset, bytes;
+};
+
+Sizes sizes_of(const KarpoAttnArgs* a, const Geometry& g) {
+  Sizes z;
+  z.tiles = tile_capacity(a, g);
+  z.items = z.tiles + split_slots(g);
+  z.merges = ka_min(z.tiles, split_tiles(g));
+  z.plan_entries = kPlanHeader + kMergeInts * z.merges + kItemInts * z.items;
+  const int64_t ints = z.plan_entries + (int64_t)a->n_seq + 1;  // plan, then the planner's tile bases
+  z.partial_offset = (ints * 4 + 255) / 256 * 256;
+  const int64_t partial = split_slots(g) * g.n_hg * (int64_t)g.vectors * (a->head_dim + 2) * 4;
+  z.bytes = z.partial_offset + (partial + 255) / 256 * 256;
+  return z;
+}
+
 int check_stride(int64_t s) { return s >= 0 && s % 8 == 0; }
 
 }  // namespace
 
-extern "C" int karpo_attn_version(void) { return 1; }
+extern "C" int karpo_attn_version(void) { return 2; }
 
 extern "C" const char* karpo_attn_strerror(int status) {
   switch (status) {
@@ -59,11 +78,12 @@ extern "C" const char* karpo_attn_strerror(int status) {
   }
 }
 
-extern "C" int karpo_attn_tile_shape(int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t* rows_per_tile,
-                                     int32_t* keys_per_step, int32_t* heads_per_item) {
+extern "C" int karpo_attn_tile_shape(int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t max_q,
+                                     int32_t* rows_per_tile, int32_t* keys_per_step, int32_t* heads_per_item) {
   if (heads < 1 || kv_heads < 1 || heads % kv_heads != 0) return KARPO_ATTN_ERR_HEADS;
   if (!head_dim_supported(head_dim)) return KARPO_ATTN_ERR_HEAD_DIM;
-  const Geometry g = geometry(heads, kv_heads, head_dim);
+  if (max_q < 0) return KARPO_ATTN_ERR_ARG;
+  const Geometry g = geometry(heads, kv_heads, head_dim, max_q);
   if (rows_per_tile) *rows_per_tile = g.rows;
   if (keys_per_step) *keys_per_step = g.bn;
   if (heads_per_item) *heads_per_item = g.ng;
@@ -74,18 +94,15 @@ extern "C" int karpo_attn_plan_capacity(const KarpoAttnArgs* a, int64_t* entries
   const int st = check_shape(a);
   if (st != KARPO_ATTN_OK) return st;
   if (entries == nullptr) return KARPO_ATTN_ERR_NULL;
-  const Geometry g = geometry(a->heads, a->kv_heads, a->head_dim);
-  *entries = kPlanHeader + 2 * tile_capacity(a, g);
+  *entries = sizes_of(a, geometry(a->heads, a->kv_heads, a->head_dim, a->max_q)).plan_entries;
   return KARPO_ATTN_OK;
 }
 
 extern "C" int karpo_attn_workspace_bytes(const KarpoAttnArgs* a, size_t* bytes) {
-  int64_t entries = 0;
-  const int st = karpo_attn_plan_capacity(a, &entries);
+  const int st = check_shape(a);
   if (st != KARPO_ATTN_OK) return st;
   if (bytes == nullptr) return KARPO_ATTN_ERR_NULL;
-  const int64_t ints = entries + (int64_t)a->n_seq + 1;
-  *bytes = (size_t)((ints * 4 + 255) / 256 * 256);
+  *bytes = (size_t)sizes_of(a, geometry(a->heads, a->kv_heads, a->head_dim, a->max_q)).bytes;
   return KARPO_ATTN_OK;
 }
 
@@ -101,26 +118,28 @@ extern "C" int karpo_attn_fwd(const KarpoAttnArgs* a, void* stream) {
       !check_stride(a->o_stride_tok) || !check_stride(a->o_stride_head))
     return KARPO_ATTN_ERR_LAYOUT;
 
-  const Geometry g = geometry(a->heads, a->kv_heads, a->head_dim);
+  const Geometry g = geometry(a->heads, a->kv_heads, a->head_dim, a->max_q);
   // a step's key rows are addressed with 32-bit byte offsets
   if ((a->k_stride_tok + a->head_dim) * g.bn * 2 >= (int64_t)INT32_MAX ||
       (a->v_stride_tok + a->head_dim) * g.bn * 2 >= (int64_t)INT32_MAX)
     return KARPO_ATTN_ERR_LAYOUT;
-  const int64_t cap = tile_capacity(a, g);
-  if (cap > (int64_t)INT32_MAX / 4 || cap * g.n_hg > (int64_t)INT32_MAX) return KARPO_ATTN_ERR_ARG;
+  const Sizes z = sizes_of(a, g);
+  if (z.plan_entries > (int64_t)INT32_MAX / 2 || z.items * g.n_hg > (int64_t)INT32_MAX) return KARPO_ATTN_ERR_ARG;
+  // a host plan that splits no tile needs neither the planner's space nor partials
+  const bool merge = split_slots(g) >= 2 && !(a->plan != nullptr && a->plan_unsplit != 0);
+  if ((a->plan == nullptr || merge) &&
+      (a->workspace == nullptr || a->workspace_bytes < (size_t)z.bytes || !aligned16(a->workspace)))
+    return KARPO_ATTN_ERR_WORKSPACE;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(a->workspace);
 
   const int32_t* plan = a->plan;
   if (plan == nullptr) {
-    size_t need = 0;
-    karpo_attn_workspace_bytes(a, &need);
-    if (a->workspace == nullptr || a->workspace_bytes < need) return KARPO_ATTN_ERR_WORKSPACE;
-    int32_t* ws = static_cast<int32_t*>(a->workspace);
-    int32_t* tile_base = ws + kPlanHeader + 2 * cap;
-    if (launch_plan(a->q_cu, a->k_cu, a->n_seq, g, a->window_left, a->window_right, ws, (int)cap, tile_base, s) !=
-        hipSuccess)
+    int32_t* dplan = reinterpret_cast<int32_t*>(ws);
+    if (launch_plan(a->q_cu, a->k_cu, a->n_seq, g, a->window_left, a->window_right, dplan, (int)z.tiles,
+                    (int)z.merges, (int)z.items, dplan + z.plan_entries, s) != hipSuccess)
       return KARPO_ATTN_ERR_LAUNCH;
-    plan = ws;
+    plan = dplan;
   }
 
   Params p;
@@ -142,6 +161,8 @@ extern "C" int karpo_attn_fwd(const KarpoAttnArgs* a, void* stream) {
   p.spans = a->spans;
   p.n_spans = a->n_spans;
   p.plan = plan;
+  p.partial = ws != nullptr ? reinterpret_cast<float*>(ws + z.partial_offset) : nullptr;
+  p.slots = merge ? (int32_t)split_slots(g) : 0;  // 0: a split item (none in such a plan) would write nothing
   p.group = a->heads / a->kv_heads;
   p.ng = g.ng;
   p.n_hg = g.n_hg;
@@ -151,6 +172,7 @@ extern "C" int karpo_attn_fwd(const KarpoAttnArgs* a, void* stream) {
   float c = fabsf(a->scale) * 1.4426950408889634f;
   p.c = c > 1e-30f ? c : 1e-30f;
   p.qsign = a->scale < 0.f ? 0x80008000u : 0u;
-  if (launch_forward(p, a->head_dim, cap * g.n_hg, s) != hipSuccess) return KARPO_ATTN_ERR_LAUNCH;
+  if (launch_forward(p, a->head_dim, g, z.items, merge ? z.merges : 0, s) != hipSuccess)
+    return KARPO_ATTN_ERR_LAUNCH;
   return KARPO_ATTN_OK;
 }

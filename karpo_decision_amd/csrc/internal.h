@@ -18,6 +18,8 @@ struct Params {
   const int32_t* __restrict__ k_cu;
   const int32_t* __restrict__ spans;
   const int32_t* __restrict__ plan;
+  float* __restrict__ partial;  // per split part and head group: O [vectors][D], then m [vectors], l [vectors]
+  int32_t slots;                // partial slots per head group the buffer holds
   int32_t n_spans;
   int32_t group;    // heads / kv_heads
   int32_t ng;       // query heads per work item
@@ -27,12 +29,14 @@ struct Params {
   uint32_t qsign;   // 0x80008000 to negate Q (negative scale), else 0
 };
 
-// The attention kernel over `grid` workgroups (plan tiles x head groups) on `stream`.
-hipError_t launch_forward(const Params& p, int head_dim, int64_t grid, hipStream_t stream);
+// The attention kernel over `items` x head groups workgroups, then (when `merges` > 0) the merge kernel over
+// `merges` x head groups, on `stream`.
+hipError_t launch_forward(const Params& p, int head_dim, const Geometry& g, int64_t items, int64_t merges,
+                          hipStream_t stream);
 
-// The device planner: writes the work list for the bounds into `plan` (capacity tiles) using `tile_base`
-// (n_seq + 1 ints) as scratch.
+// The device planner: writes the work list for the bounds into `plan` (room for `merges` split tiles and `items`
+// items; at most `tiles` tiles are planned) using `tile_base` (n_seq + 1 ints) as scratch.
 hipError_t launch_plan(const int32_t* q_cu, const int32_t* k_cu, int n_seq, const Geometry& g, int left, int right,
-                       int32_t* plan, int capacity, int32_t* tile_base, hipStream_t stream);
+                       int32_t* plan, int tiles, int merges, int items, int32_t* tile_base, hipStream_t stream);
 
 }  // namespace karpo

@@ -1,9 +1,19 @@
-// Tile geometry and the per-tile cost shared by the host planner (plan.cpp) and the device planner (attn_fwd.hip).
+// Tile geometry, per-tile cost and the key-split policy shared by the host planner (plan.cpp) and the device
+// planner (attn_fwd.hip).
 //
-// A work item is one query tile of one segment for one group of query heads. A tile holds 128 query vectors (32 per
-// wave of a 4-wave workgroup); a vector is one (position, head) pair. When the GQA
-// group size G divides `vectors`, a tile covers vectors / G positions of all G heads of one key/value head, so one
-// staged K/V tile serves every head of the group; otherwise a tile covers `vectors` positions of one query head.
+// A work item is one query tile of one segment for one group of query heads, over all or one part of the key steps
+// the tile visits. A tile holds 32 query vectors per wave of its workgroup; a vector is one (position, head) pair.
+// When the GQA group size G divides the tile's vectors, a tile covers vectors / G positions of all G heads of one
+// key/value head, so one staged K/V tile serves every head of the group; otherwise it covers `vectors` positions of
+// one query head.
+//
+// Two tile shapes per head size:
+//   * wide (prefill): several waves share one K/V stream (12 at head_dim 128, 8 at 256, 4 at 64);
+//   * narrow (decode-shaped packs, every sequence's queries fit one wave's 32 vectors, e.g. the markers-only layer
+//     with one query per sequence): one wave per workgroup, several workgroups per CU.
+// A tile whose key steps exceed the pack's per-workgroup share is split into parts over its key steps; each part
+// writes an fp32 partial (O, running max, sum) and a merge kernel combines them. This bounds the critical path of
+// small packs (few long tiles) and gives decode-shaped packs the parallelism of their keys.
 #pragma once
 #include <stdint.h>
 
@@ -24,53 +34,96 @@ namespace karpo {
 #ifndef KA_BN128
 #define KA_BN128 64
 #endif
-// Waves per workgroup (each holds 32 query vectors of the tile) and keys per step, per head size.
-KA_HD constexpr int tile_waves(int head_dim) { return head_dim == 128 ? KA_W128 : head_dim == 256 ? KA_W256 : 4; }
-KA_HD constexpr int tile_keys(int head_dim) { return head_dim == 128 ? KA_BN128 : head_dim == 256 ? 32 : 64; }
-constexpr int kPlanHeader = 4;       // int32 header of a plan: tiles, rows per tile, keys per step, heads per item
+// Waves per workgroup (each holds 32 query vectors of the tile), keys per step and workgroups resident per CU (the
+// register and LDS budget of the kernel), per head size and tile shape.
+KA_HD constexpr int tile_waves(int head_dim, bool narrow) {
+  return narrow ? 1 : head_dim == 128 ? KA_W128 : head_dim == 256 ? KA_W256 : 4;
+}
+KA_HD constexpr int tile_keys(int head_dim, bool narrow) {
+  return head_dim == 64 ? 64 : head_dim == 256 ? 32 : narrow ? 32 : KA_BN128;
+}
+KA_HD constexpr int tiles_per_cu(int head_dim, bool narrow) {
+  // narrow: two K and two V tiles of tile_keys x head_dim bf16 per workgroup in 160 KiB of LDS
+  return narrow ? (head_dim == 256 ? 2 : 5) : head_dim == 64 ? 4 : 1;
+}
+constexpr int kComputeUnits = 256;   // MI355X
+constexpr int kPlanHeader = 8;       // int32 header of a plan (see karpo_attn.h)
+constexpr int kItemInts = 4;         // per work item: segment, tile, part | parts << 16, first partial slot or -1
+constexpr int kMergeInts = 4;        // per split tile: segment, tile, parts, first partial slot
 constexpr int kCostBuckets = 2048;   // device planner's cost histogram (costs clamp to the last bucket)
+constexpr int kMinSplitSteps = 8;    // only tiles longer than this split (a merge costs a few steps' time)
 
 struct Geometry {
+  bool narrow;   // one-wave tiles
+  int waves;     // waves per workgroup
   int vectors;   // query vectors per tile
   int bn;        // keys per step
   int ng;        // query heads per work item
   int rows;      // query positions per tile
   int n_hg;      // work items per tile (head groups)
+  int conc;      // workgroups the GPU runs at once
 };
 
 KA_HD inline bool head_dim_supported(int d) { return d == 64 || d == 128 || d == 256; }
 
-KA_HD inline Geometry geometry(int heads, int kv_heads, int head_dim) {
+KA_HD inline Geometry geometry_of(int heads, int kv_heads, int head_dim, bool narrow) {
   Geometry g;
-  g.vectors = 32 * tile_waves(head_dim);
-  g.bn = tile_keys(head_dim);
-  int group = heads / kv_heads;
+  g.narrow = narrow;
+  g.waves = tile_waves(head_dim, narrow);
+  g.vectors = 32 * g.waves;
+  g.bn = tile_keys(head_dim, narrow);
+  const int group = heads / kv_heads;
   g.ng = (g.vectors % group == 0) ? group : 1;
   g.rows = g.vectors / g.ng;
   g.n_hg = heads / g.ng;
+  g.conc = kComputeUnits * tiles_per_cu(head_dim, narrow);
   return g;
+}
+
+// The narrow shape when every sequence's queries (max_q) fit one narrow tile, else the wide one.
+KA_HD inline Geometry geometry(int heads, int kv_heads, int head_dim, int64_t max_q) {
+  const Geometry n = geometry_of(heads, kv_heads, head_dim, true);
+  return max_q <= n.rows ? n : geometry_of(heads, kv_heads, head_dim, false);
 }
 
 KA_HD inline int64_t ka_min(int64_t a, int64_t b) { return a < b ? a : b; }
 KA_HD inline int64_t ka_max(int64_t a, int64_t b) { return a > b ? a : b; }
 
 // Key steps a tile visits: keys [lo, hi) any query of tile t can see under the (left, right) window with the
-// bottom-right alignment (query i sits at key i + lk - lq), in steps of bn aligned to the segment's first key, plus one
-// for the tile's own store. Spans are not counted (they only reorder equal work slightly).
-KA_HD inline int tile_cost(int lq, int lk, int t, int rows, int bn, int left, int right) {
+// bottom-right alignment (query i sits at key i + lk - lq), in steps of bn aligned to the segment's first key; 0 when
+// its queries see no key. Spans are not counted (they widen a few tiles' envelopes; the kernel finds the exact one).
+KA_HD inline int64_t tile_steps(int lq, int lk, int64_t t, int rows, int bn, int left, int right) {
   const int64_t delta = (int64_t)lk - lq;
-  int64_t p0 = (int64_t)t * rows;
+  int64_t p0 = t * rows;
   int64_t p1 = ka_min((int64_t)lq, p0 + rows) - 1;
   // queries that see at least one key: i' + right >= 0 and i' - left < lk (i' = p + delta)
   if (right >= 0) p0 = ka_max(p0, -(int64_t)right - delta);
   if (left >= 0) p1 = ka_min(p1, (int64_t)lk + left - 1 - delta);
-  if (lk <= 0 || p1 < p0) return 1;
+  if (lk <= 0 || p1 < p0) return 0;
   const int64_t lo = left < 0 ? 0 : ka_max(0, p0 + delta - left);
   const int64_t hi = right < 0 ? (int64_t)lk : ka_min((int64_t)lk, p1 + delta + right + 1);
-  if (hi <= lo) return 1;
-  return (int)((hi + bn - 1) / bn - lo / bn) + 1;
+  if (hi <= lo) return 0;
+  return (hi + bn - 1) / bn - lo / bn;
 }
 
 KA_HD inline int64_t tiles_of(int64_t lq, int rows) { return lq <= 0 ? 0 : (lq + rows - 1) / rows; }
+
+// Split policy. With `total` = sum over tiles of steps x head groups (the pack's workgroup-steps), a part is at most
+// tau = max(kMinSplitSteps, ceil(total / conc)) steps: no workgroup's work exceeds the GPU's average share, so the
+// longest-first schedule ends within about two shares. Only tiles longer than tau split, so the parts of split tiles
+// number below 2 * total / (tau * n_hg) <= 2 * conc / n_hg: the partial buffer has a size fixed by the geometry.
+KA_HD inline int64_t split_tau(int64_t total, int conc) {
+  const int64_t tau = (total + conc - 1) / conc;
+  return tau < kMinSplitSteps ? kMinSplitSteps : tau;
+}
+KA_HD inline int split_parts(int64_t steps, int64_t tau) { return steps > tau ? (int)((steps + tau - 1) / tau) : 1; }
+// Ordering cost of one part of a tile: its steps, plus one for the store (clamped to the histogram).
+KA_HD inline int part_cost(int64_t steps, int parts) {
+  const int64_t c = (steps + parts - 1) / parts + 1;
+  return (int)ka_min(c, kCostBuckets - 1);
+}
+// Partial slots (per head group) the parts of split tiles can take, and the split tiles there can be.
+KA_HD inline int64_t split_slots(const Geometry& g) { return 2 * (int64_t)g.conc / g.n_hg; }
+KA_HD inline int64_t split_tiles(const Geometry& g) { return split_slots(g) / 2; }
 
 }  // namespace karpo

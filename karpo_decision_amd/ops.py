@@ -57,7 +57,7 @@ def check_inputs(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_cu: 
 
 def _args(query: Tensor, key: Tensor, value: Tensor, out: Tensor | None, q_cu: Tensor | None, k_cu: Tensor | None,
           n_seq: int, max_q: int, scale: float, window_left: int, window_right: int, spans: Tensor | None,
-          plan: Tensor | None) -> _lib.KarpoAttnArgs:
+          plan: Tensor | None, plan_split_tiles: int = -1) -> _lib.KarpoAttnArgs:
     a = _lib.KarpoAttnArgs()
     a.q, a.k, a.v = query.data_ptr(), key.data_ptr(), value.data_ptr()
     a.o = out.data_ptr() if out is not None else 0
@@ -76,17 +76,18 @@ def _args(query: Tensor, key: Tensor, value: Tensor, out: Tensor | None, q_cu: T
     if spans is not None and spans.numel():
         a.spans, a.n_spans = spans.data_ptr(), spans.shape[0]
     a.plan = plan.data_ptr() if plan is not None else 0
+    a.plan_unsplit = 1 if plan is not None and plan_split_tiles == 0 else 0
     return a
 
 
 @torch.library.custom_op(f"{NAMESPACE}::packed_attention", mutates_args=())
 def packed_attention(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_cu: Tensor, max_q: int,
                      scale: float, window_left: int, window_right: int, spans: Tensor | None,
-                     plan: Tensor | None) -> Tensor:
+                     plan: Tensor | None, plan_split_tiles: int = -1) -> Tensor:
     """(Tq, heads, D) bf16: sequence i's query rows q_cu[i]:q_cu[i+1] over its key rows k_cu[i]:k_cu[i+1] (bounds
     int32 on the device), query i at key coordinate i + Lk - Lq, seeing keys j with i' - left <= j <= i' + right
     (-1: unbounded), or in its own span (``spans`` (n, 2) int32 query-row ranges); ``plan`` a device work list from
-    ``make_plan`` or None (planned on the device)."""
+    ``make_plan`` or None (planned on the device), ``plan_split_tiles`` its split-tile count when known (-1)."""
     check_inputs(query, key, value, q_cu, k_cu)
     if query.device.type != "cuda":
         raise ValueError(f"packed attention runs on an MI355X GPU, not on {query.device}")
@@ -102,11 +103,12 @@ def packed_attention(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_
     q_cu, k_cu = q_cu.contiguous(), k_cu.contiguous()
     with torch.cuda.device(query.device):
         args = _args(query, key, value, out, q_cu, k_cu, q_cu.numel() - 1, max_q, scale, window_left, window_right,
-                     spans, plan)
+                     spans, plan, plan_split_tiles)
         workspace = None
-        if plan is None:
+        if not args.plan_unsplit:
             need = ctypes.c_size_t()
             _lib.check(lib.karpo_attn_workspace_bytes(ctypes.byref(args), ctypes.byref(need)), "packed attention")
+            # the device plan and the fp32 partials of split tiles, from the caching allocator (stream-ordered reuse)
             workspace = torch.empty(need.value, dtype=torch.uint8, device=query.device)
             args.workspace, args.workspace_bytes = workspace.data_ptr(), need.value
         stream = torch.cuda.current_stream(query.device).cuda_stream
@@ -115,14 +117,14 @@ def packed_attention(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_
 
 
 @packed_attention.register_fake
-def _(query, key, value, q_cu, k_cu, max_q, scale, window_left, window_right, spans, plan):
+def _(query, key, value, q_cu, k_cu, max_q, scale, window_left, window_right, spans, plan, plan_split_tiles=-1):
     return query.new_empty(query.shape)
 
 
 @dataclass(frozen=True)
 class Plan:
     """A pack's work list on the device, built once on the host (like ``block_plan``'s bounds,
-    families/gemma/packed.py:103-151) and reused by every layer of the same head geometry and window."""
+    families/gemma/packed.py:103-151) and reused by every layer of the same head geometry, window and tile shape."""
 
     tensor: Tensor
     heads: int
@@ -130,41 +132,60 @@ class Plan:
     head_dim: int
     window_left: int
     window_right: int
-    tiles: int
+    max_q: int
+    items: int
     rows_per_tile: int
+    split_tiles: int
+
+    @property
+    def header(self) -> list[int]:
+        return self.tensor[:8].tolist()
 
 
 def make_plan(q_cu: list[int] | Tensor, k_cu: list[int] | Tensor, heads: int, kv_heads: int, head_dim: int,
-              window_left: int = -1, window_right: int = -1, device: torch.device | str = "cuda") -> Plan:
-    """The longest-first work list for host bounds ``q_cu`` / ``k_cu`` (lists or CPU tensors), on ``device``."""
+              window_left: int = -1, window_right: int = -1, device: torch.device | str = "cuda",
+              max_q: int | None = None) -> Plan:
+    """The longest-first work list for host bounds ``q_cu`` / ``k_cu`` (lists or CPU tensors), on ``device``.
+    ``max_q`` (default: the longest query run) must be the value the calls pass: it selects the tile shape."""
     qc = [int(x) for x in (q_cu.tolist() if isinstance(q_cu, Tensor) else q_cu)]
     kc = [int(x) for x in (k_cu.tolist() if isinstance(k_cu, Tensor) else k_cu)]
     if len(qc) != len(kc) or not qc:
         raise ValueError("q_cu and k_cu must hold the same, non-zero number of bounds")
+    n = len(qc) - 1
+    longest = max((qc[i + 1] - qc[i] for i in range(n)), default=0)
+    if max_q is None:
+        max_q = longest
+    if max_q < longest:
+        raise ValueError(f"max_q {max_q} is below the longest query run {longest}")
     lib = _lib.load()
     a = _lib.KarpoAttnArgs()
     a.heads, a.kv_heads, a.head_dim = heads, kv_heads, head_dim
     a.window_left, a.window_right = window_left, window_right
-    n = len(qc) - 1
-    rows, _, _ = _lib.tile_shape(heads, kv_heads, head_dim)
-    capacity = 4 + 2 * sum(max(0, -(-(qc[i + 1] - qc[i]) // rows)) for i in range(n))
+    a.n_seq, a.total_q, a.max_q = n, qc[-1] - qc[0], max_q
+    entries = ctypes.c_int64()
+    _lib.check(lib.karpo_attn_plan_capacity(ctypes.byref(a), ctypes.byref(entries)), "karpo_attn_plan_capacity")
     qa = (ctypes.c_int32 * len(qc))(*qc)
     ka = (ctypes.c_int32 * len(kc))(*kc)
-    buf = (ctypes.c_int32 * capacity)()
-    _lib.check(lib.karpo_attn_plan(ctypes.byref(a), qa, ka, n, buf, capacity), "karpo_attn_plan")
-    host = torch.tensor(list(buf), dtype=torch.int32)
-    return Plan(host.to(device), heads, kv_heads, head_dim, window_left, window_right, int(buf[0]), int(buf[1]))
+    buf = (ctypes.c_int32 * entries.value)()
+    _lib.check(lib.karpo_attn_plan(ctypes.byref(a), qa, ka, n, buf, entries.value), "karpo_attn_plan")
+    used = buf[6] + 4 * buf[0]
+    host = torch.tensor(list(buf[:used]), dtype=torch.int32)
+    return Plan(host.to(device), heads, kv_heads, head_dim, window_left, window_right, max_q, int(buf[0]),
+                int(buf[1]), int(buf[4]))
 
 
 def run(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_cu: Tensor, max_q: int, scale: float,
         window_left: int = -1, window_right: int = -1, spans: Tensor | None = None,
         plan: Plan | None = None) -> Tensor:
     """``packed_attention`` with a ``Plan`` checked against the call's geometry."""
-    tensor = None
+    tensor, split_tiles = None, -1
     if plan is not None:
         if (plan.heads, plan.kv_heads, plan.head_dim, plan.window_left, plan.window_right) != (
                 query.shape[1], key.shape[1], query.shape[2], window_left, window_right):
             raise ValueError("the plan was made for another head geometry or window")
-        tensor = plan.tensor
+        if _lib.tile_shape(plan.heads, plan.kv_heads, plan.head_dim, plan.max_q) != _lib.tile_shape(
+                plan.heads, plan.kv_heads, plan.head_dim, int(max_q)):
+            raise ValueError(f"the plan was made for max_q {plan.max_q}, another tile shape than max_q {max_q}")
+        tensor, split_tiles = plan.tensor, plan.split_tiles
     return packed_attention(query, key, value, q_cu, k_cu, int(max_q), float(scale), int(window_left),
-                            int(window_right), spans, tensor)
+                            int(window_right), spans, tensor, split_tiles)

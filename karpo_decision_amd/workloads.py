@@ -64,6 +64,10 @@ class Workload:
         """HBM bytes the op must move at least: read Q, K, V once, write O (bf16)."""
         return 2 * (2 * self.query.numel() + self.key.numel() + self.value.numel())
 
+    def bound(self, ridge: float) -> str:
+        """"mfma" when the algorithmic FLOPs per byte exceed the roofline's ridge point, else "hbm"."""
+        return "mfma" if self.flops() / self.bytes() > ridge else "hbm"
+
     def describe(self) -> dict:
         return {"workload": self.name, "tokens": self.tokens, "segments": len(self.q_cu) - 1, "heads": self.heads,
                 "kv_heads": self.kv_heads, "head_dim": self.head_dim, "window_left": self.window_left,
@@ -167,15 +171,32 @@ def gemma_global(length: int = 32768, device="cuda", seed: int = 0) -> Workload:
                     seed=seed)
 
 
+def _multimodal_lengths(rng: np.random.Generator, tokens: int, segments: int) -> np.ndarray:
+    raw = np.exp(rng.normal(math.log(900), SIGMA, size=segments))
+    lengths = np.maximum(16, np.floor(raw / raw.sum() * tokens)).astype(np.int64)
+    lengths[np.argmax(lengths)] += tokens - int(lengths.sum())
+    return lengths
+
+
+def markers_only(device="cuda", seed: int = 0, tokens: int = 65536, segments: int = 48) -> Workload:
+    """The markers-only last global layer (families/gemma/packed.py:267-281) of the mixed 65,536-token pack: one
+    query per virtual sequence over all of its keys, bidirectional, 32 / 16 heads, D 128. Decode-shaped: every key is
+    read once and used by the group's two query heads, so the bound is HBM bandwidth."""
+    lengths = _multimodal_lengths(np.random.default_rng(seed), tokens, segments)
+    k_cu = bounds([int(x) for x in lengths])
+    m_cu = bounds([1] * segments)
+    q, _, _ = make_tensors(segments, 32, 16, 128, seed + 1, device)
+    _, k, v = make_tensors(tokens, 32, 16, 128, seed, device)
+    return Workload(f"markers-only-{tokens}", q, k, v, m_cu, k_cu, 1 / math.sqrt(128), -1, -1, seed=seed)
+
+
 def mixed_multimodal(device="cuda", seed: int = 0, tokens: int = 65536, segments: int = 48,
                      image_segments: int = 12, span: int = 560) -> Workload:
     """65,536 tokens in 48 log-normal segments (median 900, scaled to sum exactly); 12 segments carry one or two
     560-row image spans at seeded non-overlapping offsets; causal plus bidirectional within each span; 32 / 16
     heads, D 128."""
     rng = np.random.default_rng(seed)
-    raw = np.exp(rng.normal(math.log(900), SIGMA, size=segments))
-    lengths = np.maximum(16, np.floor(raw / raw.sum() * tokens)).astype(np.int64)
-    lengths[np.argmax(lengths)] += tokens - int(lengths.sum())
+    lengths = _multimodal_lengths(rng, tokens, segments)
     cu = bounds([int(x) for x in lengths])
     eligible = [i for i in range(segments) if lengths[i] >= span]
     chosen = sorted(rng.choice(eligible, size=min(image_segments, len(eligible)), replace=False).tolist())
@@ -203,6 +224,7 @@ def named(name: str, device="cuda", seed: int = 0) -> Workload:
         "global32k": lambda: gemma_global(32768, device, seed),
         "global131k": lambda: gemma_global(131072, device, seed),
         "multimodal": lambda: mixed_multimodal(device, seed),
+        "markers": lambda: markers_only(device, seed),
     }
     if name not in table:
         raise ValueError(f"unknown workload {name!r}; one of {sorted(table)}")

@@ -278,32 +278,92 @@ def _c_abi_call(q, k, v, o, q_cu, k_cu, max_q, scale, left, right, plan=None):
     return ws
 
 
+def _plan_parts(plan: torch.Tensor) -> tuple[list[int], list[tuple], list[tuple]]:
+    """(header, merges, items) of a plan in the layout of karpo_attn.h."""
+    plan = plan.cpu()
+    header = plan[:8].tolist()
+    merges = [tuple(x) for x in plan[8: 8 + 4 * header[4]].view(-1, 4).tolist()]
+    items = [tuple(x) for x in plan[header[6]: header[6] + 4 * header[0]].view(-1, 4).tolist()]
+    return header, merges, items
+
+
 def test_every_row_is_written_and_device_plan_matches_host_plan(gpu):
     """Through the C ABI: an output pre-filled with NaN has no NaN left; the device planner's work list is the host
-    planner's as a multiset, ordered by non-increasing cost; running from the host plan gives the same bits."""
+    planner's (same header and split tiles, the same items as a multiset, ordered by non-increasing cost); running
+    from the host plan gives the same bits. The Qwen-class pack is small enough that its longest tiles split."""
     w = workloads.qwen_full(gpu, seed=7)
     q_cu = torch.tensor(w.q_cu, dtype=torch.int32, device=gpu)
     o = torch.full_like(w.query, float("nan"))
     ws = _c_abi_call(w.query, w.key, w.value, o, q_cu, q_cu, w.max_q, w.scale, -1, 0)
     assert not torch.isnan(o).any()
     plan = ops.make_plan(w.q_cu, w.k_cu, w.heads, w.kv_heads, w.head_dim, -1, 0, device=gpu)
-    dev = ws.view(torch.int32)[: plan.tensor.numel()].cpu()
-    host = plan.tensor.cpu()
-    assert dev[:4].tolist() == host[:4].tolist()
-    pairs_dev = sorted(map(tuple, dev[4:].view(-1, 2).tolist()))
-    pairs_host = sorted(map(tuple, host[4:].view(-1, 2).tolist()))
-    assert pairs_dev == pairs_host
+    host_header, host_merges, host_items = _plan_parts(plan.tensor)
+    dev_header, dev_merges, dev_items = _plan_parts(ws.view(torch.int32)[: plan.tensor.numel()])
+    assert host_header[4] > 0, "expected split tiles in this pack"
+    assert dev_header == host_header
+    assert dev_merges == host_merges
+    assert sorted(dev_items) == sorted(host_items)
     # non-increasing cost along the device list (causal self-attention: steps 0 .. the tile's last row)
-    rows, bn = host[1].item(), host[2].item()
+    rows, bn = host_header[1], host_header[2]
     costs = []
-    for seg, t in dev[4:].view(-1, 2).tolist():
+    for seg, t, pp, _ in dev_items:
         lq = w.q_cu[seg + 1] - w.q_cu[seg]
-        p1 = min(lq, (t + 1) * rows) - 1
-        costs.append(-(-(p1 + 1) // bn) + 1)
+        steps = -(-min(lq, (t + 1) * rows) // bn)
+        parts = pp >> 16
+        costs.append(-(-steps // parts) + 1)
     assert all(a >= b for a, b in zip(costs, costs[1:]))
     o2 = torch.empty_like(w.query)
     _c_abi_call(w.query, w.key, w.value, o2, q_cu, q_cu, w.max_q, w.scale, -1, 0, plan=plan.tensor)
     assert torch.equal(o, o2)
+
+
+def _lengths_cu(lengths):
+    cu = [0]
+    for n in lengths:
+        cu.append(cu[-1] + n)
+    return cu
+
+
+@pytest.mark.parametrize("heads,kv_heads,head", [(32, 16, 128), (32, 4, 256), (16, 8, 256), (8, 2, 64), (10, 2, 128)])
+def test_markers_only_layer(gpu, heads, kv_heads, head):
+    """The markers-only global layer (families/gemma/packed.py:267-281): one query per virtual sequence over all of
+    its keys, bidirectional, max_q = 1, through the reference-shaped hook. One-wave tiles, key steps split across
+    the GPU and merged; compared with the oracle on every row, and every row written (NaN-filled, C ABI)."""
+    torch.manual_seed(10 + head)
+    k_lens = [32768, 7000, 1, 0, 300, 4097]
+    k_cu = _lengths_cu(k_lens)
+    m_cu = _lengths_cu([1 if n else 0 for n in k_lens])
+    q = torch.randn(m_cu[-1], heads, head, device=gpu).bfloat16()
+    k = torch.randn(k_cu[-1], kv_heads, head, device=gpu).bfloat16()
+    v = torch.randn(k_cu[-1], kv_heads, head, device=gpu).bfloat16()
+    mc, kc = (torch.tensor(x, dtype=torch.int32, device=gpu) for x in (m_cu, k_cu))
+    scale = head ** -0.5
+    with torch.inference_mode():
+        got = hip_attention.attend(q, k, v, mc, kc, 1, scale)
+    want = oa.packed_attention(q.cpu(), k.cpu(), v.cpu(), m_cu, k_cu, scale, -1, -1)
+    assert_close(got, want, f"markers {heads}/{kv_heads}/{head}")
+    o = torch.full_like(q, float("nan"))
+    _c_abi_call(q, k, v, o, mc, kc, 1, scale, -1, -1)
+    assert torch.equal(o, got)
+
+
+@pytest.mark.parametrize("left", [-1, 1023])
+@pytest.mark.parametrize("heads,kv_heads,head", [(32, 16, 128), (16, 8, 256)])
+def test_decode_shaped_causal_pack(gpu, heads, kv_heads, head, left):
+    """Few queries per sequence over long key runs with the bottom-right alignment (branches, chunked prefill):
+    causal and windowed, one-wave tiles when every sequence's queries fit one wave, wide tiles otherwise."""
+    torch.manual_seed(11)
+    k_lens = [9000, 40, 3000, 1, 17000]
+    for q_lens in ([1, 1, 1, 1, 1], [7, 3, 16, 1, 12], [40, 17, 33, 1, 5]):
+        q_cu, k_cu = _lengths_cu(q_lens), _lengths_cu(k_lens)
+        q = torch.randn(q_cu[-1], heads, head, device=gpu).bfloat16()
+        k = torch.randn(k_cu[-1], kv_heads, head, device=gpu).bfloat16()
+        v = torch.randn(k_cu[-1], kv_heads, head, device=gpu).bfloat16()
+        qc, kc = (torch.tensor(x, dtype=torch.int32, device=gpu) for x in (q_cu, k_cu))
+        with torch.inference_mode():
+            got = ops.run(q, k, v, qc, kc, max(q_lens), 0.08, left, 0)
+        want = oa.packed_attention(q.cpu(), k.cpu(), v.cpu(), q_cu, k_cu, 0.08, left, 0)
+        assert_close(got, want, f"decode {heads}/{kv_heads}/{head} left {left} q {q_lens}")
 
 
 def test_reference_shaped_entry_points(gpu):

@@ -29,32 +29,57 @@ def test_library_exports_every_declared_function():
     assert set(names) == set(_lib.EXPORTS)
     for name in names:
         assert hasattr(lib, name), name
-    assert lib.karpo_attn_version() == 1
+    assert lib.karpo_attn_version() == 2
 
 
-def host_plan(q_cu, k_cu, heads, kv_heads, head_dim, left, right):
+def host_plan(q_cu, k_cu, heads, kv_heads, head_dim, left, right, max_q=_lib.LONG):
+    """(header, merges, items) of karpo_attn_plan's output: merges (segment, tile, parts, slot); items
+    (segment, tile, part, parts) with the item's slot checked against its tile's merge entry."""
     lib = _lib.load()
     a = _lib.KarpoAttnArgs()
     a.heads, a.kv_heads, a.head_dim, a.window_left, a.window_right = heads, kv_heads, head_dim, left, right
-    cap = 4 + 2 * 4096
+    a.n_seq, a.total_q, a.max_q = len(q_cu) - 1, q_cu[-1], max_q
+    entries = ctypes.c_int64()
+    _lib.check(lib.karpo_attn_plan_capacity(ctypes.byref(a), ctypes.byref(entries)), "capacity")
+    cap = entries.value
     buf = (ctypes.c_int32 * cap)()
     n = len(q_cu) - 1
     st_ = lib.karpo_attn_plan(ctypes.byref(a), (ctypes.c_int32 * len(q_cu))(*q_cu),
                               (ctypes.c_int32 * len(k_cu))(*k_cu), n, buf, cap)
     _lib.check(st_, "plan")
-    tiles = buf[0]
-    return list(buf[:4]), [(buf[4 + 2 * i], buf[5 + 2 * i]) for i in range(tiles)]
+    header = list(buf[:8])
+    merges = [tuple(buf[8 + 4 * i: 12 + 4 * i]) for i in range(header[4])]
+    slot_of = {(m[0], m[1]): m[3] for m in merges}
+    items = []
+    for i in range(header[0]):
+        seg, tile, pp, slot = buf[header[6] + 4 * i: header[6] + 4 * i + 4]
+        part, parts = pp & 0xFFFF, pp >> 16
+        assert slot == (slot_of[(seg, tile)] if parts > 1 else -1)
+        items.append((seg, tile, part, parts))
+    return header, merges, items
 
 
+#: Workgroups one CU runs at once, per (head_dim, one-wave tiles): the register and LDS budgets of the kernels.
+TILES_PER_CU = {(64, False): 4, (128, False): 1, (256, False): 1, (64, True): 5, (128, True): 5, (256, True): 2}
 GEOMETRIES = [(8, 2, 64), (16, 8, 128), (32, 16, 128), (16, 8, 256), (12, 4, 128), (10, 2, 128), (4, 4, 64)]
 
 
-@settings(max_examples=60, deadline=None)
+def expected_plan(q_cu, k_cu, heads, kv_heads, head_dim, left, right, max_q):
+    rows, bn, per = _lib.tile_shape(heads, kv_heads, head_dim, max_q)
+    narrow = rows * per == 32
+    conc = 256 * TILES_PER_CU[(head_dim, narrow)]
+    merges, items = schedule.split_plan(q_cu, k_cu, rows, bn, left, right, heads // per, conc)
+    return rows, bn, per, narrow, merges, items
+
+
+@settings(max_examples=80, deadline=None)
 @given(q_lens=st.lists(st.integers(0, 700), min_size=1, max_size=5),
        extra=st.lists(st.integers(-200, 300), min_size=5, max_size=5),
        geom=st.sampled_from(GEOMETRIES), left=st.sampled_from([-1, 0, 5, 64, 300]),
-       right=st.sampled_from([-1, 0, 3]))
-def test_host_plan_matches_brute_force(q_lens, extra, geom, left, right):
+       right=st.sampled_from([-1, 0, 3]), short=st.booleans())
+def test_host_plan_matches_brute_force(q_lens, extra, geom, left, right, short):
+    if short:  # decode-shaped: a few queries per sequence over longer key runs
+        q_lens = [q % 5 for q in q_lens]
     k_lens = [max(0, q + e) for q, e in zip(q_lens, extra)]
     q_cu = [0]
     k_cu = [0]
@@ -62,11 +87,43 @@ def test_host_plan_matches_brute_force(q_lens, extra, geom, left, right):
         q_cu.append(q_cu[-1] + a)
         k_cu.append(k_cu[-1] + b)
     heads, kv_heads, head_dim = geom
-    rows, bn, per = _lib.tile_shape(heads, kv_heads, head_dim)
-    header, items = host_plan(q_cu, k_cu, heads, kv_heads, head_dim, left, right)
-    assert header == [len(items), rows, bn, per]
-    want = schedule.work_list(q_cu, k_cu, rows, bn, left, right)
-    assert items == [(seg, t) for _, seg, t in want]
+    max_q = max(q_lens)
+    rows, bn, per, narrow, merges, items = expected_plan(q_cu, k_cu, heads, kv_heads, head_dim, left, right, max_q)
+    header, got_merges, got_items = host_plan(q_cu, k_cu, heads, kv_heads, head_dim, left, right, max_q)
+    waves = 1 if narrow else (32 * 0 + rows * per) // 32
+    assert header[:7] == [len(items), rows, bn, per, len(merges), waves, 8 + 4 * len(merges)]
+    assert header[7] == sum(m[2] for m in merges)
+    assert got_merges == merges
+    assert got_items == items
+    # every part of a split tile is listed once; the slots of split tiles do not overlap
+    for seg, tile, parts, slot in merges:
+        assert sorted(q for s_, t, q, n in items if (s_, t) == (seg, tile)) == list(range(parts))
+    assert header[7] <= 2 * 256 * TILES_PER_CU[(head_dim, narrow)] // (heads // per)
+
+
+def test_split_bound_is_tight_enough():
+    # one long causal segment in a pack of 16 KV heads: the parts of split tiles stay within the fixed slot budget
+    for lens in ([2210, 1547, 1138, 861, 680, 666, 526, 351, 213], [8192], [1] * 64, [3000, 5]):
+        q_cu = [0]
+        for n in lens:
+            q_cu.append(q_cu[-1] + n)
+        for heads, kv, d in ((16, 8, 128), (32, 16, 128), (16, 8, 256), (8, 2, 64)):
+            header, merges, items = host_plan(q_cu, q_cu, heads, kv, d, -1, 0, max(lens))
+            rows, bn, per = _lib.tile_shape(heads, kv, d, max(lens))
+            narrow = rows * per == 32
+            assert header[7] <= 2 * 256 * TILES_PER_CU[(d, narrow)] // (heads // per)
+
+
+def test_markers_plan_splits_keys():
+    # markers-only shape: one query per sequence over all of its keys (bidirectional) takes one-wave tiles whose
+    # key steps are split across the GPU
+    k_cu = [0, 32768, 40000]
+    q_cu = [0, 1, 2]
+    header, merges, items = host_plan(q_cu, k_cu, 32, 16, 128, -1, -1, 1)
+    assert header[1:4] == [16, 32, 2] and header[5] == 1
+    # 1024 + 226 steps of 32 keys x 16 head groups over 5 x 256 one-wave workgroups: parts of 16 steps
+    assert merges == [(0, 0, 64, 0), (1, 0, 15, 64)]
+    assert len(items) == 79 and header[7] == 79
 
 
 def test_tile_geometry():
@@ -77,6 +134,13 @@ def test_tile_geometry():
     assert _lib.tile_shape(16, 8, 256) == (128, 32, 2)
     assert _lib.tile_shape(12, 4, 128) == (128, 64, 3)  # a group of 3 divides 384 vectors
     assert _lib.tile_shape(10, 2, 128) == (384, 64, 1)  # a group of 5 does not: one head per item
+    # one-wave tiles when every sequence's queries fit 32 vectors
+    assert _lib.tile_shape(32, 16, 128, 1) == (16, 32, 2)
+    assert _lib.tile_shape(32, 16, 128, 16) == (16, 32, 2)
+    assert _lib.tile_shape(32, 16, 128, 17) == (192, 64, 2)
+    assert _lib.tile_shape(32, 4, 256, 4) == (4, 32, 8)
+    assert _lib.tile_shape(8, 2, 64, 8) == (8, 64, 4)
+    assert _lib.tile_shape(10, 2, 128, 32) == (32, 32, 1)
 
 
 def test_plan_refuses_bad_bounds_and_small_buffers():
@@ -118,6 +182,7 @@ def _args(**kw):
     (dict(k_stride_tok=130), _lib.ERR_LAYOUT),
     (dict(q=0), 1),
     (dict(), 5),  # no workspace and no plan
+    (dict(plan=1 << 22), 5),  # a host plan that may split tiles needs the partials' workspace
 ])
 def test_fwd_refuses_before_launch(change, status):
     lib = _lib.load()
@@ -137,17 +202,26 @@ def test_workspace_and_capacity():
     a = _args(n_seq=3, total_q=1000, max_q=600)
     entries, size = ctypes.c_int64(), ctypes.c_size_t()
     assert lib.karpo_attn_plan_capacity(ctypes.byref(a), ctypes.byref(entries)) == 0
-    rows, _, _ = _lib.tile_shape(4, 2, 64)
+    rows, _, per = _lib.tile_shape(4, 2, 64)
     tiles = min(-(-1000 // rows) + 3, 3 * -(-600 // rows))
-    assert entries.value == 4 + 2 * tiles
+    slots = 2 * 256 * TILES_PER_CU[(64, False)] // (4 // per)
+    assert entries.value == 8 + 4 * min(tiles, slots // 2) + 4 * (tiles + slots)
     assert lib.karpo_attn_workspace_bytes(ctypes.byref(a), ctypes.byref(size)) == 0
-    assert size.value >= 4 * (entries.value + 4) and size.value % 256 == 0
+    partial = slots * (4 // per) * 128 * (64 + 2) * 4
+    assert size.value >= 4 * (entries.value + 4) + partial and size.value % 256 == 0
 
 
 def test_python_plan_object():
     plan = ops.make_plan([0, 100, 400], [0, 100, 400], 32, 16, 128, -1, 0, device="cpu")
-    assert plan.tiles == 1 + 2 and plan.rows_per_tile == 192
-    assert plan.tensor.dtype.is_signed and plan.tensor.numel() == 4 + 2 * plan.tiles
+    # tiles of 2, 3 and 5 key steps, none longer than the shortest split (8 steps)
+    assert plan.items == 3 and plan.rows_per_tile == 192 and plan.split_tiles == 0
+    assert plan.tensor.dtype.is_signed and plan.tensor.numel() == 8 + 4 * plan.items
+    assert plan.header == [3, 192, 64, 2, 0, 12, 8, 0]
+    long = ops.make_plan([0, 3000], [0, 3000], 32, 16, 128, -1, 0, device="cpu")
+    # 16 tiles of 3, 6, .., 45 and 47 steps: 407 x 16 = 6512 workgroup-steps over 256, parts of at most 26 steps
+    assert long.split_tiles == 8 and long.items == 16 + 8
+    with pytest.raises(ValueError):
+        ops.make_plan([0, 100, 400], [0, 100, 400], 32, 16, 128, -1, 0, device="cpu", max_q=10)
 
 
 @pytest.mark.parametrize("q_cu,k_cu,left,right,spans", [
