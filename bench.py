@@ -41,6 +41,9 @@ def parse() -> argparse.Namespace:
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-repeats", type=int, default=3)
+    p.add_argument("--materialize-gather", action="store_true",
+                   help="for workloads with a gather table: time index_select copies of K/V plus the attention on "
+                        "them (the reference's Packed._gather path) instead of reading through the table")
     p.add_argument("--copy-bytes", type=int, default=0,
                    help="after the timed steps, copy this many bytes device to device once (a calibration kernel of "
                         "known traffic for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -57,9 +60,10 @@ def cpu_baseline(w, repeats: int) -> dict:
 
     torch.set_num_threads(int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)))
     group = w.heads // w.kv_heads
+    key, value = w.gathered()
     q = w.query[:, :group].cpu()
-    k = w.key[:, :1].cpu()
-    v = w.value[:, :1].cpu()
+    k = key[:, :1].cpu()
+    v = value[:, :1].cpu()
     sample_flops = w.flops() * group / w.heads
     best = None
     times_by_dtype = {}
@@ -110,10 +114,15 @@ def main() -> int:
     k_cu = torch.tensor(w.k_cu, dtype=torch.int32, device=device)
     spans = torch.tensor(w.spans, dtype=torch.int32, device=device) if w.spans else None
     plan = ops.make_plan(w.q_cu, w.k_cu, w.heads, w.kv_heads, w.head_dim, w.window_left, w.window_right, device)
+    rows = (torch.tensor(w.key_rows, dtype=torch.int32, device=device) if w.key_rows is not None else None)
 
     def step():
+        if rows is not None and args.materialize_gather:
+            key, value = w.key.index_select(0, rows), w.value.index_select(0, rows)
+            return ops.run(w.query, key, value, q_cu, k_cu, w.max_q, w.scale, w.window_left, w.window_right, spans,
+                           plan)
         return ops.run(w.query, w.key, w.value, q_cu, k_cu, w.max_q, w.scale, w.window_left, w.window_right, spans,
-                       plan)
+                       plan, rows)
 
     with torch.inference_mode():
         for _ in range(args.warmup):
@@ -163,7 +172,9 @@ def main() -> int:
         "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
-        "config": {**w.describe(), "pct_of_bf16_peak": round(100 * value / PEAK_BF16_TFLOPS, 2),
+        "config": {**w.describe(), **({"gather": "index_select copies" if args.materialize_gather else "fused"}
+                                      if rows is not None else {}),
+                   "pct_of_bf16_peak": round(100 * value / PEAK_BF16_TFLOPS, 2),
                    "tokens_per_s": round(w.tokens / (ms_per_step * 1e-3)), "flops_per_step": flops,
                    "min_hbm_bytes_per_step": w.bytes(), "parallelism": "single GPU"},
         "roofline": {**roof, "traffic": traffic,

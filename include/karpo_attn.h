@@ -14,6 +14,7 @@
  *   - src/karpo_decision/families/gemma/global_attention.py:71-79    padded(query, key, value, cu, size, causal, scale)
  *   - src/karpo_decision/families/gemma/vision.py:198-210            see_whole(...) (image spans, folded into the mask)
  *   - src/karpo_decision/families/gemma/packed.py:103-151            block_plan (the per-pack plan; karpo_attn_plan)
+ *   - src/karpo_decision/families/gemma/packed.py:222-226            _gather (index_select of branch keys; k_rows)
  *
  * Conventions: every pointer argument marked "device" is HIP device memory; sizes and strides are in elements;
  * bf16 is passed as raw 16-bit storage. No entry point allocates, synchronises or copies between host and device;
@@ -77,6 +78,10 @@ typedef struct KarpoAttnArgs {
   size_t workspace_bytes;
   int32_t plan_unsplit;  /* nonzero when args->plan splits no tile (its plan[4] == 0): the merge kernel is not
                             launched. 0 (always safe) when unknown. Ignored without a plan. */
+  const int32_t* k_rows; /* device, k_cu[n_seq] row indices, or NULL: key j of sequence i is row k_rows[k_cu[i] + j]
+                            of k and v (the gathered branch keys of a block plan, read in place) instead of row
+                            k_cu[i] + j. Rows outside [0, total_k) read as zeros. */
+  int64_t total_k;       /* rows of k and v; required with k_rows (the rows' byte span must stay below 4 GiB) */
 } KarpoAttnArgs;
 
 /* Bytes of device workspace karpo_attn_fwd needs for these arguments (reads only sizes: heads, kv_heads, head_dim,

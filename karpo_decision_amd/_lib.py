@@ -33,7 +33,7 @@ class KarpoAttnArgs(ctypes.Structure):
         ("window_left", ctypes.c_int32), ("window_right", ctypes.c_int32),
         ("spans", ctypes.c_void_p), ("n_spans", ctypes.c_int32),
         ("plan", ctypes.c_void_p), ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
-        ("plan_unsplit", ctypes.c_int32),
+        ("plan_unsplit", ctypes.c_int32), ("k_rows", ctypes.c_void_p), ("total_k", ctypes.c_int64),
     ]
 
 

@@ -131,7 +131,7 @@ __device__ __forceinline__ void dma_16b(const uint16_t* base, int bytes, KA_LDS 
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (KA_LDS void*)lds, 16, voff, 0, 0, 0);
 }
 
-template <int D, bool NARROW>
+template <int D, bool NARROW, bool GATHER>
 __global__ __launch_bounds__((64 * TileCfg<D, NARROW>::W), (TileCfg<D, NARROW>::OCC)) void attn_fwd_kernel(Params p) {
   constexpr int W = TileCfg<D, NARROW>::W;  // waves of the workgroup
   constexpr int BN = TileCfg<D, NARROW>::BN;
@@ -257,32 +257,67 @@ __global__ __launch_bounds__((64 * TileCfg<D, NARROW>::W), (TileCfg<D, NARROW>::
   // ---- DMA: per instruction a lane's byte offset inside the step's rows (fixed for the kernel). Each step's rows
   // are one buffer resource starting at the step's first key row, sized to the rows that exist: reads past the
   // sequence's last key return zeros, so no per-step address arithmetic runs on the VALU.
-  const uint16_t* kbase = p.k + (int64_t)kvh * p.sk_h + (int64_t)ka * p.sk_t;
-  const uint16_t* vbase = p.v + (int64_t)kvh * p.sv_h + (int64_t)ka * p.sv_t;
+  // Gathered keys (GATHER): a lane's row comes from the row table; the table entries of the step a copy issues are
+  // loaded one step ahead (the end-of-step wait covers them), rows past the sequence or outside [0, total_k) get an
+  // offset past the buffer and read as zeros.
+  const uint16_t* kbase = p.k + (int64_t)kvh * p.sk_h + (GATHER ? 0 : (int64_t)ka * p.sk_t);
+  const uint16_t* vbase = p.v + (int64_t)kvh * p.sv_h + (GATHER ? 0 : (int64_t)ka * p.sv_t);
+  constexpr int GI = GATHER ? INSTS : 1;
   uint32_t k_voff[INSTS], v_voff[INSTS];
+  int k_key[GI], v_key[GI], k_row[GI], v_row[GI];
 #pragma unroll
   for (int r = 0; r < INSTS; ++r) {
     int key, colm;
     k_dma_source<D>(wave * INSTS + r, lane, &key, &colm);
-    k_voff[r] = (uint32_t)(key * p.sk_t + colm) * 2u;
+    if constexpr (GATHER) {
+      k_key[r] = key;
+      k_voff[r] = (uint32_t)colm * 2u;
+    } else {
+      k_voff[r] = (uint32_t)(key * p.sk_t + colm) * 2u;
+    }
     v_dma_source<D>(wave * INSTS + r, lane, &key, &colm);
-    v_voff[r] = (uint32_t)(key * p.sv_t + colm) * 2u;
+    if constexpr (GATHER) {
+      v_key[r] = key;
+      v_voff[r] = (uint32_t)colm * 2u;
+    } else {
+      v_voff[r] = (uint32_t)(key * p.sv_t + colm) * 2u;
+    }
   }
+  auto fetch_rows = [&](int j0) {  // GATHER: the table rows of step j0's copy
+    if constexpr (GATHER) {
+#pragma unroll
+      for (int r = 0; r < INSTS; ++r) {
+        k_row[r] = j0 + k_key[r] < lk ? p.k_rows[ka + j0 + k_key[r]] : -1;
+        v_row[r] = j0 + v_key[r] < lk ? p.k_rows[ka + j0 + v_key[r]] : -1;
+      }
+    }
+  };
+  auto gathered = [&](int row, uint32_t colb, int64_t stride) -> uint32_t {
+    return (unsigned)row < (unsigned)p.total_k ? (uint32_t)row * (uint32_t)(stride * 2) + colb : 0xffffffffu;
+  };
   auto copy_k = [&](int j0, KA_LDS char* kt) {
     const int rows = min(lk - j0, BN);
-    const uint16_t* ks = kbase + (int64_t)j0 * p.sk_t;
+    const uint16_t* ks = kbase + (GATHER ? 0 : (int64_t)j0 * p.sk_t);
 #pragma unroll
     for (int r = 0; r < INSTS; ++r)
-      if (BLKS % W == 0 || wave * INSTS + r < BLKS)
-        dma_16b(ks, rows * (int)p.sk_t * 2, kt + (wave * INSTS + r) * 1024, k_voff[r]);
+      if (BLKS % W == 0 || wave * INSTS + r < BLKS) {
+        if constexpr (GATHER)
+          dma_16b(ks, (int)p.k_bytes, kt + (wave * INSTS + r) * 1024, gathered(k_row[r], k_voff[r], p.sk_t));
+        else
+          dma_16b(ks, rows * (int)p.sk_t * 2, kt + (wave * INSTS + r) * 1024, k_voff[r]);
+      }
   };
   auto copy_v = [&](int j0, KA_LDS char* vt) {
     const int rows = min(lk - j0, BN);
-    const uint16_t* vs = vbase + (int64_t)j0 * p.sv_t;
+    const uint16_t* vs = vbase + (GATHER ? 0 : (int64_t)j0 * p.sv_t);
 #pragma unroll
     for (int r = 0; r < INSTS; ++r)
-      if (BLKS % W == 0 || wave * INSTS + r < BLKS)
-        dma_16b(vs, rows * (int)p.sv_t * 2, vt + (wave * INSTS + r) * 1024, v_voff[r]);
+      if (BLKS % W == 0 || wave * INSTS + r < BLKS) {
+        if constexpr (GATHER)
+          dma_16b(vs, (int)p.v_bytes, vt + (wave * INSTS + r) * 1024, gathered(v_row[r], v_voff[r], p.sv_t));
+        else
+          dma_16b(vs, rows * (int)p.sv_t * 2, vt + (wave * INSTS + r) * 1024, v_voff[r]);
+      }
   };
   auto copy_step = [&](int j0, KA_LDS char* kt, KA_LDS char* vt) {
     copy_k(j0, kt);
@@ -305,8 +340,12 @@ __global__ __launch_bounds__((64 * TileCfg<D, NARROW>::W), (TileCfg<D, NARROW>::
   KA_LDS char* const kt1 = (KA_LDS char*)k_lds1;
   KA_LDS char* const vt0 = (KA_LDS char*)v_lds0;
   KA_LDS char* const vt1 = (KA_LDS char*)v_lds1;
-  // prologue: the first step in flight, wait for it
-  if (n_steps > 0) copy_step(j_first, kt0, vt0);
+  // prologue: the first step in flight (and the second's table rows), wait for it
+  if (n_steps > 0) {
+    fetch_rows(j_first);
+    copy_step(j_first, kt0, vt0);
+    if (n_steps > 1) fetch_rows(j_first + BN);
+  }
   wait_vmcnt<0>();
   __syncthreads();
 
@@ -314,6 +353,7 @@ __global__ __launch_bounds__((64 * TileCfg<D, NARROW>::W), (TileCfg<D, NARROW>::
   auto step = [&](int s, const KA_LDS char* kt, const KA_LDS char* vt, KA_LDS char* kn, KA_LDS char* vn) {
     const int j0 = j_first + s * BN;
     if (s + 1 < n_steps) copy_step(j0 + BN, kn, vn);
+    if (GATHER && s + 2 < n_steps) fetch_rows(j0 + 2 * BN);
     if (j0 < whi && j0 + BN > wlo) {  // wave-uniform: some query of this wave sees a key of this step
       f32x16 st[KB];
 #pragma unroll
@@ -654,8 +694,12 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* __res
 
 template <int D, bool NARROW>
 static hipError_t launch_attn(const Params& p, int64_t items, int64_t merges, int n_hg, hipStream_t stream) {
-  hipLaunchKernelGGL((attn_fwd_kernel<D, NARROW>), dim3((unsigned)(items * n_hg)),
-                     dim3(64 * TileCfg<D, NARROW>::W), 0, stream, p);
+  if (p.k_rows != nullptr)
+    hipLaunchKernelGGL((attn_fwd_kernel<D, NARROW, true>), dim3((unsigned)(items * n_hg)),
+                       dim3(64 * TileCfg<D, NARROW>::W), 0, stream, p);
+  else
+    hipLaunchKernelGGL((attn_fwd_kernel<D, NARROW, false>), dim3((unsigned)(items * n_hg)),
+                       dim3(64 * TileCfg<D, NARROW>::W), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || merges <= 0) return e;
   constexpr int64_t per_merge = (int64_t)32 * TileCfg<D, NARROW>::W * (D / 4);  // threads of one head group

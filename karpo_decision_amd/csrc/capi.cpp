@@ -123,6 +123,12 @@ extern "C" int karpo_attn_fwd(const KarpoAttnArgs* a, void* stream) {
   if ((a->k_stride_tok + a->head_dim) * g.bn * 2 >= (int64_t)INT32_MAX ||
       (a->v_stride_tok + a->head_dim) * g.bn * 2 >= (int64_t)INT32_MAX)
     return KARPO_ATTN_ERR_LAYOUT;
+  if (a->k_rows != nullptr) {  // gathered rows are addressed with 32-bit byte offsets from each head's first element
+    if (a->total_k < 1 || a->total_k > INT32_MAX) return KARPO_ATTN_ERR_ARG;
+    const int64_t kspan = (a->total_k - 1) * a->k_stride_tok + a->head_dim;
+    const int64_t vspan = (a->total_k - 1) * a->v_stride_tok + a->head_dim;
+    if (kspan * 2 >= (int64_t)UINT32_MAX - 16 || vspan * 2 >= (int64_t)UINT32_MAX - 16) return KARPO_ATTN_ERR_LAYOUT;
+  }
   const Sizes z = sizes_of(a, g);
   if (z.plan_entries > (int64_t)INT32_MAX / 2 || z.items * g.n_hg > (int64_t)INT32_MAX) return KARPO_ATTN_ERR_ARG;
   // a host plan that splits no tile needs neither the planner's space nor partials
@@ -161,6 +167,12 @@ extern "C" int karpo_attn_fwd(const KarpoAttnArgs* a, void* stream) {
   p.spans = a->spans;
   p.n_spans = a->n_spans;
   p.plan = plan;
+  p.k_rows = a->k_rows;
+  if (a->k_rows != nullptr) {
+    p.total_k = (int32_t)a->total_k;
+    p.k_bytes = (uint32_t)(((a->total_k - 1) * a->k_stride_tok + a->head_dim) * 2);
+    p.v_bytes = (uint32_t)(((a->total_k - 1) * a->v_stride_tok + a->head_dim) * 2);
+  }
   p.partial = ws != nullptr ? reinterpret_cast<float*>(ws + z.partial_offset) : nullptr;
   p.slots = merge ? (int32_t)split_slots(g) : 0;  // 0: a split item (none in such a plan) would write nothing
   p.group = a->heads / a->kv_heads;

@@ -18,6 +18,9 @@ struct Params {
   const int32_t* __restrict__ k_cu;
   const int32_t* __restrict__ spans;
   const int32_t* __restrict__ plan;
+  const int32_t* __restrict__ k_rows;  // gathered key rows, or null
+  uint32_t k_bytes, v_bytes;           // with k_rows: bytes from a head's first element to past the last row
+  int32_t total_k;                     // with k_rows: rows of k and v
   float* __restrict__ partial;  // per split part and head group: O [vectors][D], then m [vectors], l [vectors]
   int32_t slots;                // partial slots per head group the buffer holds
   int32_t n_spans;

@@ -8,7 +8,9 @@ Mirror of src/karpo_decision/families/gemma/triton_attention.py (``supported`` :
   ``attend`` takes keyword-only ``causal``, ``window`` and ``spans``, and ``enable`` installs a causal ``attend`` on a
   causal model;
 * offsets are 64-bit everywhere, so there is no 131,071-token cap and no 32-bit-offset ValueError;
-* GQA heads share one staged K/V tile instead of re-reading it per query head.
+* GQA heads share one staged K/V tile instead of re-reading it per query head;
+* ``rows`` reads a block plan's branch keys in place (``g_rows``, the gather ``Packed._gather`` makes with
+  ``index_select``, families/gemma/packed.py:222-226, :245).
 """
 
 from __future__ import annotations
@@ -34,16 +36,17 @@ def supported(device: torch.device) -> bool:
 
 def attend(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, q_cu: torch.Tensor, k_cu: torch.Tensor,
            max_q: int, scale: float, *, causal: bool = False, window: int = -1, spans: torch.Tensor | None = None,
-           plan: ops.Plan | None = None) -> torch.Tensor:
+           plan: ops.Plan | None = None, rows: torch.Tensor | None = None) -> torch.Tensor:
     """Attention per virtual sequence: (Lq, heads, D) bf16 queries over (Lk, kv heads, D) keys and values, sequence
     i's query rows q_cu[i]:q_cu[i+1] over its key rows k_cu[i]:k_cu[i+1] (int32 on the device), ``max_q`` at least
     its longest query range; bidirectional unless ``causal`` (aligned at each sequence's end), ``window`` keys before
     a query's own position (-1: unbounded), ``spans`` (n, 2) int32 query-row ranges that see themselves whole;
-    (Lq, heads, D)."""
+    ``rows`` (int32 / int64 on the device): key row r is row rows[r] of ``key`` / ``value`` (the branch gather, read
+    in place); (Lq, heads, D)."""
     if torch.is_grad_enabled():
         raise RuntimeError("hip_attention runs the forward only: call it under torch.inference_mode or no_grad")
     return ops.run(query, key, value, q_cu, k_cu, max_q, scale, window_left=window, window_right=0 if causal else -1,
-                   spans=spans, plan=plan)
+                   spans=spans, plan=plan, key_rows=rows)
 
 
 def enable(model: Any, max_length: int) -> None:

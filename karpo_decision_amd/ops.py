@@ -57,7 +57,7 @@ def check_inputs(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_cu: 
 
 def _args(query: Tensor, key: Tensor, value: Tensor, out: Tensor | None, q_cu: Tensor | None, k_cu: Tensor | None,
           n_seq: int, max_q: int, scale: float, window_left: int, window_right: int, spans: Tensor | None,
-          plan: Tensor | None, plan_split_tiles: int = -1) -> _lib.KarpoAttnArgs:
+          plan: Tensor | None, plan_split_tiles: int = -1, key_rows: Tensor | None = None) -> _lib.KarpoAttnArgs:
     a = _lib.KarpoAttnArgs()
     a.q, a.k, a.v = query.data_ptr(), key.data_ptr(), value.data_ptr()
     a.o = out.data_ptr() if out is not None else 0
@@ -77,17 +77,21 @@ def _args(query: Tensor, key: Tensor, value: Tensor, out: Tensor | None, q_cu: T
         a.spans, a.n_spans = spans.data_ptr(), spans.shape[0]
     a.plan = plan.data_ptr() if plan is not None else 0
     a.plan_unsplit = 1 if plan is not None and plan_split_tiles == 0 else 0
+    if key_rows is not None:
+        a.k_rows, a.total_k = key_rows.data_ptr(), key.shape[0]
     return a
 
 
 @torch.library.custom_op(f"{NAMESPACE}::packed_attention", mutates_args=())
 def packed_attention(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_cu: Tensor, max_q: int,
                      scale: float, window_left: int, window_right: int, spans: Tensor | None,
-                     plan: Tensor | None, plan_split_tiles: int = -1) -> Tensor:
+                     plan: Tensor | None, plan_split_tiles: int = -1, key_rows: Tensor | None = None) -> Tensor:
     """(Tq, heads, D) bf16: sequence i's query rows q_cu[i]:q_cu[i+1] over its key rows k_cu[i]:k_cu[i+1] (bounds
     int32 on the device), query i at key coordinate i + Lk - Lq, seeing keys j with i' - left <= j <= i' + right
     (-1: unbounded), or in its own span (``spans`` (n, 2) int32 query-row ranges); ``plan`` a device work list from
-    ``make_plan`` or None (planned on the device), ``plan_split_tiles`` its split-tile count when known (-1)."""
+    ``make_plan`` or None (planned on the device), ``plan_split_tiles`` its split-tile count when known (-1);
+    ``key_rows`` (int32 on the device) maps key row r to row key_rows[r] of ``key`` / ``value`` (a gather read in
+    place, as ``key.index_select(0, key_rows)`` would give)."""
     check_inputs(query, key, value, q_cu, k_cu)
     if query.device.type != "cuda":
         raise ValueError(f"packed attention runs on an MI355X GPU, not on {query.device}")
@@ -96,6 +100,9 @@ def packed_attention(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_
         raise ValueError("spans must be a contiguous (n, 2) int32 tensor on the query's device")
     if max_q < 0:
         raise ValueError(f"max_q must be non-negative, not {max_q}")
+    if key_rows is not None and (key_rows.dtype != torch.int32 or key_rows.dim() != 1
+                                 or key_rows.device != query.device or not key_rows.is_contiguous()):
+        raise ValueError("key_rows must be a contiguous 1-D int32 tensor on the query's device")
     lib = _lib.load()
     out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
     if query.shape[0] == 0:
@@ -103,7 +110,7 @@ def packed_attention(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_
     q_cu, k_cu = q_cu.contiguous(), k_cu.contiguous()
     with torch.cuda.device(query.device):
         args = _args(query, key, value, out, q_cu, k_cu, q_cu.numel() - 1, max_q, scale, window_left, window_right,
-                     spans, plan, plan_split_tiles)
+                     spans, plan, plan_split_tiles, key_rows)
         workspace = None
         if not args.plan_unsplit:
             need = ctypes.c_size_t()
@@ -117,7 +124,8 @@ def packed_attention(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_
 
 
 @packed_attention.register_fake
-def _(query, key, value, q_cu, k_cu, max_q, scale, window_left, window_right, spans, plan, plan_split_tiles=-1):
+def _(query, key, value, q_cu, k_cu, max_q, scale, window_left, window_right, spans, plan, plan_split_tiles=-1,
+      key_rows=None):
     return query.new_empty(query.shape)
 
 
@@ -174,10 +182,18 @@ def make_plan(q_cu: list[int] | Tensor, k_cu: list[int] | Tensor, heads: int, kv
                 int(buf[1]), int(buf[4]))
 
 
+def key_rows_of(rows: Tensor | None) -> Tensor | None:
+    """A gather table (``block_plan``'s int64 ``g_rows`` / ``s_rows``) as the int32 rows the kernel reads."""
+    if rows is None or (rows.dtype == torch.int32 and rows.is_contiguous()):
+        return rows
+    return rows.to(torch.int32).contiguous()
+
+
 def run(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_cu: Tensor, max_q: int, scale: float,
         window_left: int = -1, window_right: int = -1, spans: Tensor | None = None,
-        plan: Plan | None = None) -> Tensor:
-    """``packed_attention`` with a ``Plan`` checked against the call's geometry."""
+        plan: Plan | None = None, key_rows: Tensor | None = None) -> Tensor:
+    """``packed_attention`` with a ``Plan`` checked against the call's geometry; ``key_rows`` (int32 or int64) reads
+    the keys and values through a row table instead of a gathered copy."""
     tensor, split_tiles = None, -1
     if plan is not None:
         if (plan.heads, plan.kv_heads, plan.head_dim, plan.window_left, plan.window_right) != (
@@ -188,4 +204,4 @@ def run(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_cu: Tensor, m
             raise ValueError(f"the plan was made for max_q {plan.max_q}, another tile shape than max_q {max_q}")
         tensor, split_tiles = plan.tensor, plan.split_tiles
     return packed_attention(query, key, value, q_cu, k_cu, int(max_q), float(scale), int(window_left),
-                            int(window_right), spans, tensor, split_tiles)
+                            int(window_right), spans, tensor, split_tiles, key_rows_of(key_rows))

@@ -16,13 +16,14 @@ from . import ops
 
 def attend(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, q_cu: torch.Tensor, k_cu: torch.Tensor,
            max_q: int, max_k: int, scale: float, window: int, *, spans: torch.Tensor | None = None,
-           plan: ops.Plan | None = None) -> torch.Tensor:
+           plan: ops.Plan | None = None, rows: torch.Tensor | None = None) -> torch.Tensor:
     """(T, heads, D) queries over (Tk, kv heads, D) keys and values (``q_cu`` / ``k_cu``: int32 boundaries), each
-    query seeing at most ``window`` keys before its own position; (T, heads, D). Forward only: RuntimeError when
+    query seeing at most ``window`` keys before its own position; ``rows``: the block plan's ``s_rows`` gather read
+    in place (key row r is row rows[r] of ``key`` / ``value``); (T, heads, D). Forward only: RuntimeError when
     autograd would need a backward."""
     if torch.is_grad_enabled() and any(t.requires_grad for t in (query, key, value)):
         raise RuntimeError("sliding_attention on MI355X runs the forward only (no backward kernel)")
     if window < 0:
         raise ValueError(f"a sliding window needs a non-negative left size, not {window}")
     return ops.run(query, key, value, q_cu, k_cu, max_q, scale, window_left=window, window_right=0, spans=spans,
-                   plan=plan)
+                   plan=plan, key_rows=rows)

@@ -33,6 +33,7 @@ class Workload:
     window_right: int = 0
     spans: list[tuple[int, int]] = field(default_factory=list)
     seed: int = 0
+    key_rows: list[int] | None = None  # key row r of the pack is row key_rows[r] of key / value (a block plan's gather)
 
     @property
     def heads(self) -> int:
@@ -63,6 +64,13 @@ class Workload:
     def bytes(self) -> int:
         """HBM bytes the op must move at least: read Q, K, V once, write O (bf16)."""
         return 2 * (2 * self.query.numel() + self.key.numel() + self.value.numel())
+
+    def gathered(self) -> tuple[torch.Tensor, torch.Tensor]:
+        """(key, value) with the gather applied (the copies ``index_select`` makes), or the tensors themselves."""
+        if self.key_rows is None:
+            return self.key, self.value
+        rows = torch.tensor(self.key_rows, dtype=torch.int64, device=self.key.device)
+        return self.key.index_select(0, rows), self.value.index_select(0, rows)
 
     def bound(self, ridge: float) -> str:
         """"mfma" when the algorithmic FLOPs per byte exceed the roofline's ridge point, else "hbm"."""
@@ -171,6 +179,30 @@ def gemma_global(length: int = 32768, device="cuda", seed: int = 0) -> Workload:
                     seed=seed)
 
 
+def branched(device="cuda", seed: int = 0, prompts: int = 4, shared: int = 4096, branches: int = 4,
+             branch: int = 512) -> Workload:
+    """A block plan's global layer (families/gemma/packed.py:103-151): ``prompts`` prompts, each a ``shared``-token
+    block (its own virtual sequence) and ``branches`` branches of ``branch`` tokens whose keys are the shared rows
+    followed by their own, read through the gather table ``g_rows`` (``key_rows``) from the pack's K/V; causal,
+    32 / 16 heads, D 128."""
+    q_cu, k_cu, rows = [0], [0], []
+    at = 0
+    for _ in range(prompts):
+        own = list(range(at, at + shared))
+        q_cu.append(at + shared)
+        rows += own
+        k_cu.append(k_cu[-1] + shared)
+        at += shared
+        for _ in range(branches):
+            q_cu.append(at + branch)
+            rows += own + list(range(at, at + branch))
+            k_cu.append(k_cu[-1] + shared + branch)
+            at += branch
+    q, k, v = make_tensors(at, 32, 16, 128, seed, device)
+    return Workload(f"branched-{prompts}x{shared}+{branches}x{branch}", q, k, v, q_cu, k_cu, 1 / math.sqrt(128), -1, 0,
+                    seed=seed, key_rows=rows)
+
+
 def _multimodal_lengths(rng: np.random.Generator, tokens: int, segments: int) -> np.ndarray:
     raw = np.exp(rng.normal(math.log(900), SIGMA, size=segments))
     lengths = np.maximum(16, np.floor(raw / raw.sum() * tokens)).astype(np.int64)
@@ -225,6 +257,7 @@ def named(name: str, device="cuda", seed: int = 0) -> Workload:
         "global131k": lambda: gemma_global(131072, device, seed),
         "multimodal": lambda: mixed_multimodal(device, seed),
         "markers": lambda: markers_only(device, seed),
+        "branched": lambda: branched(device, seed),
     }
     if name not in table:
         raise ValueError(f"unknown workload {name!r}; one of {sorted(table)}")

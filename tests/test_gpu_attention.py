@@ -62,16 +62,17 @@ def run_workload(w: workloads.Workload, plan: ops.Plan | None = None, spans_t=No
     k_cu = torch.tensor(w.k_cu, dtype=torch.int32, device=dev)
     if spans_t is None and w.spans:
         spans_t = torch.tensor(w.spans, dtype=torch.int32, device=dev)
+    rows = torch.tensor(w.key_rows, dtype=torch.int32, device=dev) if w.key_rows is not None else None
     with torch.inference_mode():
         return ops.run(w.query, w.key, w.value, q_cu, k_cu, w.max_q, w.scale, w.window_left, w.window_right,
-                       spans_t, plan)
+                       spans_t, plan, rows)
 
 
 def check_workload(w: workloads.Workload, rows=None, groups=None, label=""):
     """Kernel vs oracle on ``rows`` (all when None) of the query heads of KV heads ``groups`` (all when None)."""
     got = run_workload(w)
     torch.cuda.synchronize()
-    q, k, v = w.query, w.key, w.value
+    q, (k, v) = w.query, w.gathered()
     if groups is not None:
         g = w.heads // w.kv_heads
         heads = [kv * g + i for kv in groups for i in range(g)]
@@ -127,6 +128,11 @@ def test_gemma_sliding_workload_unit_scale(gpu):
 def test_gemma_global_workload(gpu, length):
     w = workloads.gemma_global(length, gpu)
     check_workload(w, rows=sample_rows(w.q_cu, 384, 3), groups=[0, 15])
+
+
+def test_branched_workload(gpu):
+    w = workloads.branched(gpu)
+    check_workload(w, rows=sample_rows(w.q_cu, 48, seed=6), groups=[0, 15])
 
 
 def test_mixed_multimodal_workload(gpu):
@@ -434,3 +440,92 @@ def test_enable_installs_the_hook(gpu):
     m = stub(True)
     hip_attention.enable(m, 32_768)
     assert m.global_attend.keywords == {"causal": True}
+
+
+def _block_pack(prompts, window):
+    """Bounds and gather tables of a block plan (families/gemma/packed.py:103-151): per prompt a shared block (its own
+    virtual sequence) and branches whose keys are the shared rows (global) or the shared tail of window - 1 rows
+    (sliding) followed by the branch's own rows. ``prompts``: [(shared, [branch lengths])]. Returns the pack's row
+    count, q_cu, g_cu, s_cu, g_rows, s_rows (int64 lists), and m_cu (one marker per virtual sequence, its last row)."""
+    q_cu, g_cu, s_cu, g_rows, s_rows, markers = [0], [0], [0], [], [], []
+    at = 0
+    for shared, branches in prompts:
+        own = list(range(at, at + shared))
+        q_cu.append(at + shared)
+        g_rows += own
+        s_rows += own
+        g_cu.append(g_cu[-1] + shared)
+        s_cu.append(s_cu[-1] + shared)
+        markers.append(at + shared - 1)
+        tail = own[max(0, shared - (window - 1)):]
+        at += shared
+        for n in branches:
+            rows = list(range(at, at + n))
+            q_cu.append(at + n)
+            g_rows += own + rows
+            s_rows += tail + rows
+            g_cu.append(g_cu[-1] + shared + n)
+            s_cu.append(s_cu[-1] + len(tail) + n)
+            if n:
+                markers.append(at + n - 1)
+            at += n
+    m_cu = [0]
+    for a, b in zip(q_cu[:-1], q_cu[1:]):
+        m_cu.append(m_cu[-1] + (1 if b > a else 0))
+    return at, q_cu, g_cu, s_cu, g_rows, s_rows, m_cu, markers
+
+
+@pytest.mark.parametrize("heads,kv_heads,head", [(32, 16, 128), (16, 8, 256), (8, 2, 64)])
+def test_branch_keys_read_through_row_tables(gpu, heads, kv_heads, head):
+    """The fused branch gather (families/gemma/packed.py:222-226): global, sliding and markers-only calls over the
+    pack's own K/V with g_rows / s_rows equal, bit for bit, the calls on index_select copies, and match the oracle."""
+    torch.manual_seed(12 + head)
+    window = 300
+    prompts = [(1000, [37, 120, 0]), (5, [400]), (700, []), (2, [3, 1])]
+    total, q_cu, g_cu, s_cu, g_rows, s_rows, m_cu, markers = _block_pack(prompts, window)
+    q = torch.randn(total, heads, head, device=gpu).bfloat16()
+    k = torch.randn(total, kv_heads, head, device=gpu).bfloat16()
+    v = torch.randn(total, kv_heads, head, device=gpu).bfloat16()
+    qc, gc, sc, mc = (torch.tensor(x, dtype=torch.int32, device=gpu) for x in (q_cu, g_cu, s_cu, m_cu))
+    gr, sr = (torch.tensor(x, dtype=torch.int64, device=gpu) for x in (g_rows, s_rows))
+    max_q = max(b - a for a, b in zip(q_cu[:-1], q_cu[1:]))
+    max_s = max(b - a for a, b in zip(s_cu[:-1], s_cu[1:]))
+    scale = head ** -0.5
+    with torch.inference_mode():
+        fused = hip_attention.attend(q, k, v, qc, gc, max_q, scale, causal=True, rows=gr)
+        copied = hip_attention.attend(q, k[gr], v[gr], qc, gc, max_q, scale, causal=True)
+        assert torch.equal(fused, copied)
+        want = oa.packed_attention(q.cpu(), k[gr].cpu(), v[gr].cpu(), q_cu, g_cu, scale, -1, 0)
+        assert_close(fused, want, f"global gather {heads}/{kv_heads}/{head}")
+
+        fused = sliding_attention.attend(q, k, v, qc, sc, max_q, max_s, scale, window - 1, rows=sr)
+        copied = sliding_attention.attend(q, k[sr], v[sr], qc, sc, max_q, max_s, scale, window - 1)
+        assert torch.equal(fused, copied)
+        want = oa.packed_attention(q.cpu(), k[sr].cpu(), v[sr].cpu(), q_cu, s_cu, scale, window - 1, 0)
+        assert_close(fused, want, f"sliding gather {heads}/{kv_heads}/{head}")
+
+        qm = q[torch.tensor(markers, device=gpu)]
+        fused = hip_attention.attend(qm, k, v, mc, gc, 1, scale, rows=gr)
+        copied = hip_attention.attend(qm, k[gr], v[gr], mc, gc, 1, scale)
+        assert torch.equal(fused, copied)
+        want = oa.packed_attention(qm.cpu(), k[gr].cpu(), v[gr].cpu(), m_cu, g_cu, scale, -1, -1)
+        assert_close(fused, want, f"markers gather {heads}/{kv_heads}/{head}")
+
+
+def test_row_table_entries_outside_the_tensor_read_as_zero_keys(gpu):
+    """Row-table entries outside [0, total_k) read as zero keys and values (logit 0, value 0), never out of bounds."""
+    torch.manual_seed(13)
+    q = torch.randn(64, 4, 128, device=gpu).bfloat16()
+    k = torch.randn(100, 2, 128, device=gpu).bfloat16()
+    v = torch.randn(100, 2, 128, device=gpu).bfloat16()
+    rows = torch.arange(0, 100, device=gpu)
+    rows[[3, 50, 77]] = torch.tensor([-1, 100, 1 << 30], device=gpu)
+    cu = torch.tensor([0, 64], dtype=torch.int32, device=gpu)
+    kc = torch.tensor([0, 100], dtype=torch.int32, device=gpu)
+    kz, vz = k.clone(), v.clone()
+    kz[[3, 50, 77]] = 0
+    vz[[3, 50, 77]] = 0
+    with torch.inference_mode():
+        got = hip_attention.attend(q, k, v, cu, kc, 64, 0.1, causal=True, rows=rows)
+    want = oa.packed_attention(q.cpu(), kz.cpu(), vz.cpu(), [0, 64], [0, 100], 0.1, -1, 0)
+    assert_close(got, want, "out-of-range rows")
