@@ -44,7 +44,8 @@ enum {
   KARPO_ATTN_ERR_LAUNCH = 8,      /* the HIP runtime refused a launch */
   KARPO_ATTN_ERR_ARG = 9,         /* a negative size or sequence count */
   KARPO_ATTN_ERR_CAPACITY = 10,   /* karpo_attn_plan: the output buffer is too small */
-  KARPO_ATTN_ERR_BOUNDS = 11      /* karpo_attn_plan: host bounds not non-decreasing from 0 */
+  KARPO_ATTN_ERR_BOUNDS = 11,     /* karpo_attn_plan: host bounds not non-decreasing from 0 */
+  KARPO_ATTN_ERR_PROLOGUE = 12    /* a norm mode, weight, rope table or gate the kernel cannot take */
 };
 
 /* Everything one forward call needs. Tensors are bf16 with head_dim contiguous:
@@ -82,7 +83,57 @@ typedef struct KarpoAttnArgs {
                             of k and v (the gathered branch keys of a block plan, read in place) instead of row
                             k_cu[i] + j. Rows outside [0, total_k) read as zeros. */
   int64_t total_k;       /* rows of k and v; required with k_rows (the rows' byte span must stay below 4 GiB) */
+
+  /* Fused query prologue, applied to each query vector as the kernel loads it (the reference's fused.norm_rope /
+   * fused.norm on q_proj's output: families/gemma/fused.py:21-25, :41-50, :86-88; families/qwen/fused.py:17-19,
+   * :47-48):
+   *   n = bf16(q * rsqrt(mean(q^2) + q_norm_eps) * w), w = q_norm_weight[d] (KARPO_NORM_WEIGHT),
+   *       1 + q_norm_weight[d] (KARPO_NORM_ONE_PLUS) or 1 (KARPO_NORM_PLAIN), all in fp32;
+   *   then, with rope_cos, the first rope_dim elements rotate by halves in fp32:
+   *       y[d] = n[d] cos[d] - n[d + R/2] sin[d], y[d + R/2] = n[d + R/2] cos[d + R/2] + n[d] sin[d + R/2],
+   *   R = rope_dim, cos/sin rows taken at the query's row of q; the rest pass through; the result rounds to bf16. */
+  int32_t q_norm;               /* KARPO_NORM_* (KARPO_NORM_NONE: no norm) */
+  float q_norm_eps;
+  const void* q_norm_weight;    /* device bf16 [head_dim] for KARPO_NORM_WEIGHT / KARPO_NORM_ONE_PLUS */
+  const void* rope_cos;         /* device bf16 [total_q][rope_stride], or NULL: no rotation */
+  const void* rope_sin;
+  int64_t rope_stride;          /* elements between the rows of rope_cos / rope_sin (a multiple of 8) */
+  int32_t rope_dim;             /* rotated leading elements: a multiple of 32, at most head_dim */
+
+  /* Fused output gate (Qwen3.5's attention gate, families/qwen/packed.py:125, fused.py:38-39):
+   * o = bf16(bf16(o) * sigmoid(gate)) in fp32. */
+  const void* gate;             /* device bf16 [total_q][heads][head_dim] with the strides below, or NULL */
+  int64_t gate_stride_tok, gate_stride_head;
 } KarpoAttnArgs;
+
+/* Query / key normalisations of the fused prologue and of karpo_attn_norm_rope. */
+enum {
+  KARPO_NORM_NONE = 0,
+  KARPO_NORM_WEIGHT = 1,    /* Gemma4RMSNorm with a weight: x * rsqrt(mean(x^2) + eps) * w */
+  KARPO_NORM_ONE_PLUS = 2,  /* Qwen3_5RMSNorm: x * rsqrt(mean(x^2) + eps) * (1 + w) */
+  KARPO_NORM_PLAIN = 3      /* Gemma4RMSNorm without a weight (the value norm): x * rsqrt(mean(x^2) + eps) */
+};
+
+/* The prologue of karpo_attn_fwd as a pass of its own, for keys (norm and rotation) and values (norm): each
+ * (row, head) vector of x becomes y (y may be x: in place). The attention kernel stages every key tile for many
+ * query tiles, so a transform inside its key load would repeat per query tile; one pass over K here reads and writes
+ * each key once, the reference's fused.norm_rope (families/gemma/fused.py:86-88, packed.py:183-189). */
+typedef struct KarpoNormRopeArgs {
+  const void* x;                /* device bf16 [rows][heads][head_dim], head_dim contiguous */
+  void* y;                      /* device bf16, same shape */
+  int64_t x_stride_tok, x_stride_head, y_stride_tok, y_stride_head;
+  int64_t rows;
+  int32_t heads, head_dim;      /* head_dim 64, 128, 256 or 512 */
+  int32_t norm;                 /* KARPO_NORM_* */
+  float eps;
+  const void* weight;           /* device bf16 [head_dim] for KARPO_NORM_WEIGHT / KARPO_NORM_ONE_PLUS */
+  const void* rope_cos;         /* device bf16 [rows][rope_stride] or NULL */
+  const void* rope_sin;
+  int64_t rope_stride;
+  int32_t rope_dim;             /* a multiple of 32, at most head_dim */
+} KarpoNormRopeArgs;
+
+int karpo_attn_norm_rope(const KarpoNormRopeArgs* args, void* stream);
 
 /* Bytes of device workspace karpo_attn_fwd needs for these arguments (reads only sizes: heads, kv_heads, head_dim,
  * n_seq, total_q, max_q). It holds the device plan (when args->plan is NULL) and the fp32 partial results of tiles

@@ -11,12 +11,14 @@ LIBRARY = Path(__file__).resolve().parent / "libkarpo_attn.so"
 
 #: Every symbol ``include/karpo_attn.h`` declares.
 EXPORTS = ("karpo_attn_fwd", "karpo_attn_plan", "karpo_attn_plan_capacity", "karpo_attn_workspace_bytes",
-           "karpo_attn_tile_shape", "karpo_attn_strerror", "karpo_attn_version")
+           "karpo_attn_tile_shape", "karpo_attn_strerror", "karpo_attn_version", "karpo_attn_norm_rope")
 
 OK = 0
 ERR_HEAD_DIM, ERR_HEADS, ERR_LAYOUT, ERR_WINDOW, ERR_SPANS, ERR_ARG, ERR_BOUNDS = 2, 3, 4, 6, 7, 9, 11
+ERR_PROLOGUE = 12
 #: Status codes that mean "these arguments are not supported" (ValueError), the rest are runtime failures.
-VALUE_ERRORS = {1, ERR_HEAD_DIM, ERR_HEADS, ERR_LAYOUT, 5, ERR_WINDOW, ERR_SPANS, ERR_ARG, 10, ERR_BOUNDS}
+VALUE_ERRORS = {1, ERR_HEAD_DIM, ERR_HEADS, ERR_LAYOUT, 5, ERR_WINDOW, ERR_SPANS, ERR_ARG, 10, ERR_BOUNDS,
+                ERR_PROLOGUE}
 
 
 class KarpoAttnArgs(ctypes.Structure):
@@ -34,6 +36,22 @@ class KarpoAttnArgs(ctypes.Structure):
         ("spans", ctypes.c_void_p), ("n_spans", ctypes.c_int32),
         ("plan", ctypes.c_void_p), ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
         ("plan_unsplit", ctypes.c_int32), ("k_rows", ctypes.c_void_p), ("total_k", ctypes.c_int64),
+        ("q_norm", ctypes.c_int32), ("q_norm_eps", ctypes.c_float), ("q_norm_weight", ctypes.c_void_p),
+        ("rope_cos", ctypes.c_void_p), ("rope_sin", ctypes.c_void_p), ("rope_stride", ctypes.c_int64),
+        ("rope_dim", ctypes.c_int32), ("gate", ctypes.c_void_p), ("gate_stride_tok", ctypes.c_int64),
+        ("gate_stride_head", ctypes.c_int64),
+    ]
+
+
+class KarpoNormRopeArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", ctypes.c_void_p), ("y", ctypes.c_void_p),
+        ("x_stride_tok", ctypes.c_int64), ("x_stride_head", ctypes.c_int64),
+        ("y_stride_tok", ctypes.c_int64), ("y_stride_head", ctypes.c_int64),
+        ("rows", ctypes.c_int64), ("heads", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+        ("norm", ctypes.c_int32), ("eps", ctypes.c_float), ("weight", ctypes.c_void_p),
+        ("rope_cos", ctypes.c_void_p), ("rope_sin", ctypes.c_void_p), ("rope_stride", ctypes.c_int64),
+        ("rope_dim", ctypes.c_int32),
     ]
 
 
@@ -68,6 +86,8 @@ def load() -> ctypes.CDLL:
         lib.karpo_attn_strerror.restype = ctypes.c_char_p
         lib.karpo_attn_version.argtypes = []
         lib.karpo_attn_version.restype = ctypes.c_int
+        lib.karpo_attn_norm_rope.argtypes = [P(KarpoNormRopeArgs), ctypes.c_void_p]
+        lib.karpo_attn_norm_rope.restype = ctypes.c_int
         _lib = lib
         return lib
 

@@ -131,6 +131,88 @@ __device__ __forceinline__ void dma_16b(const uint16_t* base, int bytes, KA_LDS 
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (KA_LDS void*)lds, 16, voff, 0, 0, 0);
 }
 
+// ---- fused prologue / epilogue arithmetic (in fp32, rounding to bf16 where the reference's tensors are bf16)
+
+// Element e of 8 packed bf16.
+__device__ __forceinline__ float bf16_at(const u32x4& v, int e) {
+  const unsigned w = v[e >> 1];
+  return __uint_as_float((e & 1) ? (w & 0xffff0000u) : (w << 16));
+}
+__device__ __forceinline__ float round_bf16(float x) { return (float)(__bf16)x; }
+__device__ __forceinline__ unsigned pack_bf16(float a, float b) {
+  return (unsigned)__builtin_bit_cast(uint16_t, (__bf16)a) | ((unsigned)__builtin_bit_cast(uint16_t, (__bf16)b) << 16);
+}
+__device__ __forceinline__ float sigmoid(float g) { return 1.f / (1.f + __expf(-g)); }
+
+// Normalised values of 8 consecutive elements d0.. of a query row chunk (bf16-rounded, as the norm's output tensor
+// is), or the raw values when there is no norm; r = rsqrt(mean(q^2) + eps) of the whole vector.
+__device__ __forceinline__ void norm8(const Params& p, const u32x4& raw, int d0, float r, float (&n)[8]) {
+  u32x4 wv = {0, 0, 0, 0};
+  if (p.q_norm == KARPO_NORM_WEIGHT || p.q_norm == KARPO_NORM_ONE_PLUS) wv = *(const u32x4*)(p.q_norm_w + d0);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float h = bf16_at(raw, e);
+    const float w = p.q_norm == KARPO_NORM_WEIGHT ? bf16_at(wv, e)
+                    : p.q_norm == KARPO_NORM_ONE_PLUS ? 1.f + bf16_at(wv, e) : 1.f;
+    n[e] = p.q_norm != KARPO_NORM_NONE ? round_bf16(h * r * w) : h;
+  }
+}
+
+// The query prologue on one lane's half of a query vector (x[dc] holds elements dc*16 + half*8 .. +8 of the row at
+// `row`, pack row `qrow`): RMSNorm over the whole vector (the other half is in the lane 32 away), then rotation by
+// halves of the first rope_dim elements. A rotation partner is read again from the row (same lane, no exchange).
+template <int D>
+__device__ __forceinline__ void query_prologue(const Params& p, const uint16_t* row, int64_t qrow, int half,
+                                            u32x4 (&x)[D / 16]) {
+  constexpr int DC = D / 16;
+  float r = 1.f;
+  if (p.q_norm != KARPO_NORM_NONE) {
+    float ss = 0.f;
+#pragma unroll
+    for (int dc = 0; dc < DC; ++dc)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(bf16_at(x[dc], e), bf16_at(x[dc], e), ss);
+    r = 1.f / __builtin_sqrtf(half_swap_sum(ss) * (1.f / D) + p.q_eps);
+  }
+  // chunk by chunk: a rotation partner is re-read from the row, so no chunk waits on another's registers
+  const int rh = p.rope_dim >> 1;
+  const uint16_t* cr = p.rope_cos != nullptr ? p.rope_cos + qrow * p.rope_stride : nullptr;
+  const uint16_t* sr = p.rope_sin != nullptr ? p.rope_sin + qrow * p.rope_stride : nullptr;
+#pragma unroll
+  for (int dc = 0; dc < DC; ++dc) {
+    const int d0 = dc * 16 + half * 8;
+    float n[8];
+    norm8(p, x[dc], d0, r, n);
+    if (cr != nullptr && d0 < p.rope_dim) {
+      const int dp = d0 < rh ? d0 + rh : d0 - rh;
+      float pn[8];
+      norm8(p, *(const u32x4*)(row + dp), dp, r, pn);
+      const u32x4 cv = *(const u32x4*)(cr + d0), sv = *(const u32x4*)(sr + d0);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) n[e] = n[e] * bf16_at(cv, e) + (d0 < rh ? -pn[e] : pn[e]) * bf16_at(sv, e);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) x[dc][t] = pack_bf16(n[2 * t], n[2 * t + 1]);
+  }
+}
+
+// Four output elements of one query: bf16(o), then the gate's bf16(bf16(o) * sigmoid(g)) when there is one.
+__device__ __forceinline__ u32x2 output4(const Params& p, float o0, float o1, float o2, float o3,
+                                         const uint16_t* gate4) {
+  if (gate4 != nullptr) {
+    const u32x2 g = *(const u32x2*)gate4;
+    const u32x4 gv = {g[0], g[1], 0, 0};
+    o0 = round_bf16(o0) * sigmoid(bf16_at(gv, 0));
+    o1 = round_bf16(o1) * sigmoid(bf16_at(gv, 1));
+    o2 = round_bf16(o2) * sigmoid(bf16_at(gv, 2));
+    o3 = round_bf16(o3) * sigmoid(bf16_at(gv, 3));
+  }
+  u32x2 w;
+  w[0] = pack_bf16(o0, o1);
+  w[1] = pack_bf16(o2, o3);
+  return w;
+}
+
 template <int D, bool NARROW, bool GATHER>
 __global__ __launch_bounds__((64 * TileCfg<D, NARROW>::W), (TileCfg<D, NARROW>::OCC)) void attn_fwd_kernel(Params p) {
   constexpr int W = TileCfg<D, NARROW>::W;  // waves of the workgroup
@@ -226,14 +308,18 @@ __global__ __launch_bounds__((64 * TileCfg<D, NARROW>::W), (TileCfg<D, NARROW>::
 
   bf16x8 qop[DC];
   {
-    const uint16_t* qp = p.q + (int64_t)(qa + pos) * p.sq_t + (int64_t)head * p.sq_h + half * 8;
+    const uint16_t* qrow = p.q + (int64_t)(qa + pos) * p.sq_t + (int64_t)head * p.sq_h;
+    u32x4 x[DC];
 #pragma unroll
     for (int dc = 0; dc < DC; ++dc) {
-      u32x4 x = {0, 0, 0, 0};
-      if (valid) x = *(const u32x4*)(qp + dc * 16);
-      x ^= p.qsign;
-      qop[dc] = __builtin_bit_cast(bf16x8, x);
+      x[dc] = u32x4{0, 0, 0, 0};
+      if (valid) x[dc] = *(const u32x4*)(qrow + half * 8 + dc * 16);
     }
+    if (p.q_norm != KARPO_NORM_NONE || p.rope_cos != nullptr) {
+      if (valid) query_prologue<D>(p, qrow, (int64_t)(qa + pos), half, x);
+    }
+#pragma unroll
+    for (int dc = 0; dc < DC; ++dc) qop[dc] = __builtin_bit_cast(bf16x8, x[dc] ^ p.qsign);
   }
   int klo = wlo, khi = whi;
   if constexpr (W > 1) {
@@ -454,18 +540,15 @@ __global__ __launch_bounds__((64 * TileCfg<D, NARROW>::W), (TileCfg<D, NARROW>::
   const float inv = lt > 0.f ? 1.f / lt : 0.f;
   if (valid) {
     uint16_t* op = p.o + (int64_t)(qa + pos) * p.so_t + (int64_t)head * p.so_h + half * 4;
+    const uint16_t* gp =
+        p.gate != nullptr ? p.gate + (int64_t)(qa + pos) * p.sg_t + (int64_t)head * p.sg_h + half * 4 : nullptr;
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
-        u32x2 w;
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const __bf16 x0 = (__bf16)(acc[db][g4 * 4 + 2 * t] * inv);
-          const __bf16 x1 = (__bf16)(acc[db][g4 * 4 + 2 * t + 1] * inv);
-          w[t] = (unsigned)__builtin_bit_cast(uint16_t, x0) | ((unsigned)__builtin_bit_cast(uint16_t, x1) << 16);
-        }
-        *(u32x2*)(op + db * 32 + g4 * 8) = w;
+        *(u32x2*)(op + db * 32 + g4 * 8) =
+            output4(p, acc[db][g4 * 4] * inv, acc[db][g4 * 4 + 1] * inv, acc[db][g4 * 4 + 2] * inv,
+                    acc[db][g4 * 4 + 3] * inv, gp != nullptr ? gp + db * 32 + g4 * 8 : nullptr);
       }
     }
   }
@@ -517,12 +600,10 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(Params p) {
       }
     }
     const float inv = den > 0.f ? 1.f / den : 0.f;
-    const __bf16 r0 = (__bf16)(num.x * inv), r1 = (__bf16)(num.y * inv), r2 = (__bf16)(num.z * inv),
-                 r3 = (__bf16)(num.w * inv);
-    u32x2 w;
-    w[0] = (unsigned)__builtin_bit_cast(uint16_t, r0) | ((unsigned)__builtin_bit_cast(uint16_t, r1) << 16);
-    w[1] = (unsigned)__builtin_bit_cast(uint16_t, r2) | ((unsigned)__builtin_bit_cast(uint16_t, r3) << 16);
-    *(u32x2*)(p.o + (int64_t)(qa + pos) * p.so_t + (int64_t)head * p.so_h + d) = w;
+    const uint16_t* gp =
+        p.gate != nullptr ? p.gate + (int64_t)(qa + pos) * p.sg_t + (int64_t)head * p.sg_h + d : nullptr;
+    *(u32x2*)(p.o + (int64_t)(qa + pos) * p.so_t + (int64_t)head * p.so_h + d) =
+        output4(p, num.x * inv, num.y * inv, num.z * inv, num.w * inv, gp);
   }
 }
 
@@ -688,6 +769,82 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* __res
     plan[6] = first;
     plan[7] = slot_carry;
   }
+}
+
+// ---- karpo_attn_norm_rope: one wave per (row, head) vector, E = D / 64 contiguous elements per lane; the rotation
+// partner comes through the wave's LDS row.
+constexpr int kNormRopeWaves = 4;
+
+template <int D>
+__global__ __launch_bounds__(64 * kNormRopeWaves) void norm_rope_kernel(NormRopeParams p) {
+  constexpr int E = D / 64;
+  __shared__ float partner[kNormRopeWaves][D];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int64_t v = (int64_t)blockIdx.x * kNormRopeWaves + wave; v < p.vectors;
+       v += (int64_t)gridDim.x * kNormRopeWaves) {
+    const int64_t row = v / p.heads;
+    const int head = (int)(v - row * p.heads);
+    const uint16_t* xp = p.x + row * p.sx_t + (int64_t)head * p.sx_h + lane * E;
+    float h[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) h[e] = __uint_as_float((unsigned)xp[e] << 16);
+    float r = 1.f;
+    if (p.norm != KARPO_NORM_NONE) {
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < E; ++e) ss = __builtin_fmaf(h[e], h[e], ss);
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+      r = 1.f / __builtin_sqrtf(ss * (1.f / D) + p.eps);
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const float wv = p.w != nullptr ? __uint_as_float((unsigned)p.w[lane * E + e] << 16) : 0.f;
+        const float w = p.norm == KARPO_NORM_WEIGHT ? wv : p.norm == KARPO_NORM_ONE_PLUS ? 1.f + wv : 1.f;
+        h[e] = round_bf16(h[e] * r * w);
+      }
+    }
+    if (p.cos != nullptr) {
+      const int rh = p.rope_dim >> 1;
+#pragma unroll
+      for (int e = 0; e < E; ++e) partner[wave][lane * E + e] = h[e];
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+      float y[E];
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const int d = lane * E + e;
+        y[e] = h[e];
+        if (d < p.rope_dim) {
+          const float c = __uint_as_float((unsigned)p.cos[row * p.rope_stride + d] << 16);
+          const float s = __uint_as_float((unsigned)p.sin[row * p.rope_stride + d] << 16);
+          const float rot = d < rh ? -partner[wave][d + rh] : partner[wave][d - rh];
+          y[e] = h[e] * c + rot * s;
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+      for (int e = 0; e < E; ++e) h[e] = y[e];
+    }
+    uint16_t* yp = p.y + row * p.sy_t + (int64_t)head * p.sy_h + lane * E;
+#pragma unroll
+    for (int e = 0; e < E; ++e) yp[e] = __builtin_bit_cast(uint16_t, (__bf16)h[e]);
+  }
+}
+
+hipError_t launch_norm_rope(const NormRopeParams& p, int head_dim, hipStream_t stream) {
+  if (p.vectors <= 0) return hipSuccess;
+  int64_t blocks = (p.vectors + kNormRopeWaves - 1) / kNormRopeWaves;
+  if (blocks > 8192) blocks = 8192;
+  const dim3 grid((unsigned)blocks), block(64 * kNormRopeWaves);
+  switch (head_dim) {
+    case 64: hipLaunchKernelGGL(norm_rope_kernel<64>, grid, block, 0, stream, p); break;
+    case 128: hipLaunchKernelGGL(norm_rope_kernel<128>, grid, block, 0, stream, p); break;
+    case 256: hipLaunchKernelGGL(norm_rope_kernel<256>, grid, block, 0, stream, p); break;
+    case 512: hipLaunchKernelGGL(norm_rope_kernel<512>, grid, block, 0, stream, p); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 // ---- launch

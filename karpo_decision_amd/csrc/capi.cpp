@@ -54,6 +54,21 @@ Sizes sizes_of(const KarpoAttnArgs* a, const Geometry& g) {
 
 int check_stride(int64_t s) { return s >= 0 && s % 8 == 0; }
 
+bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
+
+// The fused prologue's norm, weight and rotation table (shared by karpo_attn_fwd and karpo_attn_norm_rope).
+int check_norm_rope(int norm, const void* weight, const void* cos, const void* sin, int64_t stride, int rope_dim,
+                    int head_dim) {
+  if (norm < KARPO_NORM_NONE || norm > KARPO_NORM_PLAIN) return KARPO_ATTN_ERR_PROLOGUE;
+  if ((norm == KARPO_NORM_WEIGHT || norm == KARPO_NORM_ONE_PLUS) && (weight == nullptr || !aligned16(weight)))
+    return KARPO_ATTN_ERR_PROLOGUE;
+  if ((cos == nullptr) != (sin == nullptr)) return KARPO_ATTN_ERR_PROLOGUE;
+  if (cos != nullptr && (rope_dim <= 0 || rope_dim % 32 != 0 || rope_dim > head_dim || stride < rope_dim ||
+                         stride % 8 != 0 || !aligned16(cos) || !aligned16(sin)))
+    return KARPO_ATTN_ERR_PROLOGUE;
+  return KARPO_ATTN_OK;
+}
+
 }  // namespace
 
 extern "C" int karpo_attn_version(void) { return 2; }
@@ -74,6 +89,10 @@ extern "C" const char* karpo_attn_strerror(int status) {
     case KARPO_ATTN_ERR_ARG: return "sizes and the sequence count must be non-negative";
     case KARPO_ATTN_ERR_CAPACITY: return "the plan buffer is smaller than the plan";
     case KARPO_ATTN_ERR_BOUNDS: return "sequence bounds must be non-negative and non-decreasing";
+    case KARPO_ATTN_ERR_PROLOGUE:
+      return "unsupported fused prologue / gate: norm mode 0-3 with a 16-byte aligned weight for modes 1-2, both rope "
+             "tables 16-byte aligned with a row stride that is a multiple of 8, rope_dim a multiple of 32 up to "
+             "head_dim, gate strides multiples of 4";
     default: return "unknown karpo_attn status";
   }
 }
@@ -117,6 +136,13 @@ extern "C" int karpo_attn_fwd(const KarpoAttnArgs* a, void* stream) {
       !check_stride(a->k_stride_head) || !check_stride(a->v_stride_tok) || !check_stride(a->v_stride_head) ||
       !check_stride(a->o_stride_tok) || !check_stride(a->o_stride_head))
     return KARPO_ATTN_ERR_LAYOUT;
+
+  st = check_norm_rope(a->q_norm, a->q_norm_weight, a->rope_cos, a->rope_sin, a->rope_stride, a->rope_dim,
+                       a->head_dim);
+  if (st != KARPO_ATTN_OK) return st;
+  if (a->gate != nullptr && (!aligned8(a->gate) || a->gate_stride_tok < 0 || a->gate_stride_head < 0 ||
+                             a->gate_stride_tok % 4 != 0 || a->gate_stride_head % 4 != 0))
+    return KARPO_ATTN_ERR_PROLOGUE;
 
   const Geometry g = geometry(a->heads, a->kv_heads, a->head_dim, a->max_q);
   // a step's key rows are addressed with 32-bit byte offsets
@@ -184,7 +210,51 @@ extern "C" int karpo_attn_fwd(const KarpoAttnArgs* a, void* stream) {
   float c = fabsf(a->scale) * 1.4426950408889634f;
   p.c = c > 1e-30f ? c : 1e-30f;
   p.qsign = a->scale < 0.f ? 0x80008000u : 0u;
+  p.q_norm = a->q_norm;
+  p.q_eps = a->q_norm_eps;
+  p.q_norm_w = static_cast<const uint16_t*>(a->q_norm_weight);
+  p.rope_cos = static_cast<const uint16_t*>(a->rope_cos);
+  p.rope_sin = static_cast<const uint16_t*>(a->rope_sin);
+  p.rope_stride = a->rope_stride;
+  p.rope_dim = a->rope_dim;
+  p.gate = static_cast<const uint16_t*>(a->gate);
+  p.sg_t = a->gate_stride_tok;
+  p.sg_h = a->gate_stride_head;
   if (launch_forward(p, a->head_dim, g, z.items, merge ? z.merges : 0, s) != hipSuccess)
     return KARPO_ATTN_ERR_LAUNCH;
+  return KARPO_ATTN_OK;
+}
+
+extern "C" int karpo_attn_norm_rope(const KarpoNormRopeArgs* a, void* stream) {
+  if (a == nullptr) return KARPO_ATTN_ERR_NULL;
+  if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256 && a->head_dim != 512)
+    return KARPO_ATTN_ERR_HEAD_DIM;
+  if (a->heads < 1 || a->rows < 0) return KARPO_ATTN_ERR_ARG;
+  const int st = check_norm_rope(a->norm, a->weight, a->rope_cos, a->rope_sin, a->rope_stride, a->rope_dim,
+                                 a->head_dim);
+  if (st != KARPO_ATTN_OK) return st;
+  if (a->rows == 0) return KARPO_ATTN_OK;
+  if (a->x == nullptr || a->y == nullptr) return KARPO_ATTN_ERR_NULL;
+  if (!aligned16(a->x) || !aligned16(a->y) || !check_stride(a->x_stride_tok) || !check_stride(a->x_stride_head) ||
+      !check_stride(a->y_stride_tok) || !check_stride(a->y_stride_head))
+    return KARPO_ATTN_ERR_LAYOUT;
+  NormRopeParams p;
+  memset(&p, 0, sizeof(p));
+  p.x = static_cast<const uint16_t*>(a->x);
+  p.y = static_cast<uint16_t*>(a->y);
+  p.w = static_cast<const uint16_t*>(a->weight);
+  p.cos = static_cast<const uint16_t*>(a->rope_cos);
+  p.sin = static_cast<const uint16_t*>(a->rope_sin);
+  p.sx_t = a->x_stride_tok;
+  p.sx_h = a->x_stride_head;
+  p.sy_t = a->y_stride_tok;
+  p.sy_h = a->y_stride_head;
+  p.rope_stride = a->rope_stride;
+  p.vectors = a->rows * a->heads;
+  p.heads = a->heads;
+  p.norm = a->norm;
+  p.rope_dim = a->rope_dim;
+  p.eps = a->eps;
+  if (launch_norm_rope(p, a->head_dim, static_cast<hipStream_t>(stream)) != hipSuccess) return KARPO_ATTN_ERR_LAUNCH;
   return KARPO_ATTN_OK;
 }

@@ -30,7 +30,29 @@ struct Params {
   int32_t left, right;
   float c;          // |scale| * log2(e)
   uint32_t qsign;   // 0x80008000 to negate Q (negative scale), else 0
+  // fused query prologue (norm, rotation) and output gate; see KarpoAttnArgs
+  const uint16_t* __restrict__ q_norm_w;
+  const uint16_t* __restrict__ rope_cos;
+  const uint16_t* __restrict__ rope_sin;
+  const uint16_t* __restrict__ gate;
+  int64_t rope_stride, sg_t, sg_h;
+  int32_t q_norm;
+  float q_eps;
+  int32_t rope_dim;
 };
+
+// karpo_attn_norm_rope's kernel.
+struct NormRopeParams {
+  const uint16_t* __restrict__ x;
+  uint16_t* y;
+  const uint16_t* __restrict__ w;
+  const uint16_t* __restrict__ cos;
+  const uint16_t* __restrict__ sin;
+  int64_t sx_t, sx_h, sy_t, sy_h, rope_stride, vectors;
+  int32_t heads, norm, rope_dim;
+  float eps;
+};
+hipError_t launch_norm_rope(const NormRopeParams& p, int head_dim, hipStream_t stream);
 
 // The attention kernel over `items` x head groups workgroups, then (when `merges` > 0) the merge kernel over
 // `merges` x head groups, on `stream`.

@@ -10,7 +10,10 @@ Mirror of src/karpo_decision/families/gemma/triton_attention.py (``supported`` :
 * offsets are 64-bit everywhere, so there is no 131,071-token cap and no 32-bit-offset ValueError;
 * GQA heads share one staged K/V tile instead of re-reading it per query head;
 * ``rows`` reads a block plan's branch keys in place (``g_rows``, the gather ``Packed._gather`` makes with
-  ``index_select``, families/gemma/packed.py:222-226, :245).
+  ``index_select``, families/gemma/packed.py:222-226, :245);
+* ``q_norm`` / ``cos`` / ``sin`` fuse the query's ``Gemma4RMSNorm`` and rotation (``Packed._q``, packed.py:191-193,
+  fused.norm_rope) into the kernel's query load; ``norm_rope`` / ``norm`` do the keys' and values' (``Packed._kv``,
+  :183-189) in one pass each.
 """
 
 from __future__ import annotations
@@ -36,17 +39,33 @@ def supported(device: torch.device) -> bool:
 
 def attend(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, q_cu: torch.Tensor, k_cu: torch.Tensor,
            max_q: int, scale: float, *, causal: bool = False, window: int = -1, spans: torch.Tensor | None = None,
-           plan: ops.Plan | None = None, rows: torch.Tensor | None = None) -> torch.Tensor:
+           plan: ops.Plan | None = None, rows: torch.Tensor | None = None, q_norm: Any = None,
+           cos: torch.Tensor | None = None, sin: torch.Tensor | None = None) -> torch.Tensor:
     """Attention per virtual sequence: (Lq, heads, D) bf16 queries over (Lk, kv heads, D) keys and values, sequence
     i's query rows q_cu[i]:q_cu[i+1] over its key rows k_cu[i]:k_cu[i+1] (int32 on the device), ``max_q`` at least
     its longest query range; bidirectional unless ``causal`` (aligned at each sequence's end), ``window`` keys before
     a query's own position (-1: unbounded), ``spans`` (n, 2) int32 query-row ranges that see themselves whole;
     ``rows`` (int32 / int64 on the device): key row r is row rows[r] of ``key`` / ``value`` (the branch gather, read
-    in place); (Lq, heads, D)."""
+    in place); with ``q_norm`` (a Gemma4RMSNorm module, or an ``ops.Norm``) ``query`` is q_proj's output, normalised
+    and, with ``cos`` / ``sin`` ((Lq, R) or (1, Lq, R), row i for query row i), rotated as the kernel loads it;
+    (Lq, heads, D)."""
     if torch.is_grad_enabled():
         raise RuntimeError("hip_attention runs the forward only: call it under torch.inference_mode or no_grad")
+    norm = q_norm if q_norm is None or isinstance(q_norm, ops.Norm) else ops.gemma_norm(q_norm)
+    rope = (cos, sin) if cos is not None else None
     return ops.run(query, key, value, q_cu, k_cu, max_q, scale, window_left=window, window_right=0 if causal else -1,
-                   spans=spans, plan=plan, key_rows=rows)
+                   spans=spans, plan=plan, key_rows=rows, q_norm=norm, rope=rope)
+
+
+def norm_rope(module: Any, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """``fused.norm_rope(module, x, cos, sin)`` (families/gemma/fused.py:86-88) for (1, T, heads, D) keys and
+    (1, T, D) cos / sin, in one pass on the GPU; (1, T, heads, D)."""
+    return ops.norm_rope(x[0], ops.gemma_norm(module), (cos, sin))[None]
+
+
+def norm(module: Any, x: torch.Tensor) -> torch.Tensor:
+    """``fused.norm(module, x)`` (families/gemma/fused.py:81-83) for (1, T, heads, D) values; (1, T, heads, D)."""
+    return ops.norm_rope(x[0], ops.gemma_norm(module))[None]
 
 
 def enable(model: Any, max_length: int) -> None:

@@ -19,6 +19,45 @@ from . import _lib
 
 NAMESPACE = "karpo_amd"
 
+#: Norm modes of the fused prologue (KARPO_NORM_* in karpo_attn.h).
+NORM_NONE, NORM_WEIGHT, NORM_ONE_PLUS, NORM_PLAIN = 0, 1, 2, 3
+
+
+@dataclass(frozen=True)
+class Norm:
+    """An RMSNorm the kernel applies as it loads query vectors (or ``norm_rope`` applies to keys and values):
+    ``mode`` NORM_*, ``weight`` (head_dim,) for NORM_WEIGHT / NORM_ONE_PLUS, ``eps``."""
+
+    mode: int
+    weight: Tensor | None
+    eps: float
+
+
+def gemma_norm(module) -> Norm:
+    """The fused-prologue form of a ``Gemma4RMSNorm`` (``weight`` times the normalised vector, or no weight when the
+    module has no scale: the value norm), families/gemma/fused.py:21-25, :81-88."""
+    if getattr(module, "with_scale", True):
+        return Norm(NORM_WEIGHT, module.weight, float(module.eps))
+    return Norm(NORM_PLAIN, None, float(module.eps))
+
+
+def qwen_norm(module) -> Norm:
+    """The fused-prologue form of a ``Qwen3_5RMSNorm`` (``1 + weight``), families/qwen/fused.py:17-19."""
+    return Norm(NORM_ONE_PLUS, module.weight, float(getattr(module, "eps", getattr(module, "variance_epsilon", 1e-6))))
+
+
+def _bf16_table(t: Tensor, device: torch.device) -> Tensor:
+    """A (rows, n) bf16 table with contiguous rows (norm weights, rope cos / sin), converted once if needed."""
+    if t.dim() == 3 and t.shape[0] == 1:
+        t = t[0]
+    if t.device != device:
+        raise ValueError(f"a prologue table is on {t.device}, the tensors on {device}")
+    if t.dtype != torch.bfloat16:
+        t = t.to(torch.bfloat16)
+    if t.stride(-1) != 1 or (t.dim() == 2 and t.stride(0) % 8) or t.data_ptr() % 16:
+        t = t.contiguous()
+    return t
+
 
 def _is_gfx950(device: torch.device) -> bool:
     props = torch.cuda.get_device_properties(device)
@@ -57,7 +96,9 @@ def check_inputs(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_cu: 
 
 def _args(query: Tensor, key: Tensor, value: Tensor, out: Tensor | None, q_cu: Tensor | None, k_cu: Tensor | None,
           n_seq: int, max_q: int, scale: float, window_left: int, window_right: int, spans: Tensor | None,
-          plan: Tensor | None, plan_split_tiles: int = -1, key_rows: Tensor | None = None) -> _lib.KarpoAttnArgs:
+          plan: Tensor | None, plan_split_tiles: int = -1, key_rows: Tensor | None = None, q_norm: int = 0,
+          q_norm_eps: float = 0.0, q_norm_weight: Tensor | None = None, rope_cos: Tensor | None = None,
+          rope_sin: Tensor | None = None, gate: Tensor | None = None) -> _lib.KarpoAttnArgs:
     a = _lib.KarpoAttnArgs()
     a.q, a.k, a.v = query.data_ptr(), key.data_ptr(), value.data_ptr()
     a.o = out.data_ptr() if out is not None else 0
@@ -79,19 +120,33 @@ def _args(query: Tensor, key: Tensor, value: Tensor, out: Tensor | None, q_cu: T
     a.plan_unsplit = 1 if plan is not None and plan_split_tiles == 0 else 0
     if key_rows is not None:
         a.k_rows, a.total_k = key_rows.data_ptr(), key.shape[0]
+    a.q_norm, a.q_norm_eps = q_norm, q_norm_eps
+    if q_norm_weight is not None:
+        a.q_norm_weight = q_norm_weight.data_ptr()
+    if rope_cos is not None:
+        a.rope_cos, a.rope_sin = rope_cos.data_ptr(), rope_sin.data_ptr()
+        a.rope_stride, a.rope_dim = rope_cos.stride(0), rope_cos.shape[-1]
+    if gate is not None:
+        a.gate, a.gate_stride_tok, a.gate_stride_head = gate.data_ptr(), gate.stride(0), gate.stride(1)
     return a
 
 
 @torch.library.custom_op(f"{NAMESPACE}::packed_attention", mutates_args=())
 def packed_attention(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_cu: Tensor, max_q: int,
                      scale: float, window_left: int, window_right: int, spans: Tensor | None,
-                     plan: Tensor | None, plan_split_tiles: int = -1, key_rows: Tensor | None = None) -> Tensor:
+                     plan: Tensor | None, plan_split_tiles: int = -1, key_rows: Tensor | None = None,
+                     q_norm: int = 0, q_norm_eps: float = 0.0, q_norm_weight: Tensor | None = None,
+                     rope_cos: Tensor | None = None, rope_sin: Tensor | None = None,
+                     gate: Tensor | None = None) -> Tensor:
     """(Tq, heads, D) bf16: sequence i's query rows q_cu[i]:q_cu[i+1] over its key rows k_cu[i]:k_cu[i+1] (bounds
     int32 on the device), query i at key coordinate i + Lk - Lq, seeing keys j with i' - left <= j <= i' + right
     (-1: unbounded), or in its own span (``spans`` (n, 2) int32 query-row ranges); ``plan`` a device work list from
     ``make_plan`` or None (planned on the device), ``plan_split_tiles`` its split-tile count when known (-1);
     ``key_rows`` (int32 on the device) maps key row r to row key_rows[r] of ``key`` / ``value`` (a gather read in
-    place, as ``key.index_select(0, key_rows)`` would give)."""
+    place, as ``key.index_select(0, key_rows)`` would give). Fused prologue: ``query`` is the projection's output,
+    normalised (``q_norm`` NORM_*, ``q_norm_weight`` bf16 (D,), ``q_norm_eps``) and rotated by halves over the first
+    ``rope_cos.shape[-1]`` elements (``rope_cos`` / ``rope_sin`` bf16 (Tq, R), row i for query row i) as the kernel
+    loads it; fused epilogue: the output times sigmoid(``gate``) (bf16, the output's shape)."""
     check_inputs(query, key, value, q_cu, k_cu)
     if query.device.type != "cuda":
         raise ValueError(f"packed attention runs on an MI355X GPU, not on {query.device}")
@@ -103,6 +158,18 @@ def packed_attention(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_
     if key_rows is not None and (key_rows.dtype != torch.int32 or key_rows.dim() != 1
                                  or key_rows.device != query.device or not key_rows.is_contiguous()):
         raise ValueError("key_rows must be a contiguous 1-D int32 tensor on the query's device")
+    for name, t, shape in (("q_norm_weight", q_norm_weight, (query.shape[2],)),
+                           ("rope_cos", rope_cos, None), ("rope_sin", rope_sin, None),
+                           ("gate", gate, tuple(query.shape))):
+        if t is None:
+            continue
+        if t.dtype != torch.bfloat16 or t.device != query.device:
+            raise ValueError(f"{name} must be bf16 on the query's device")
+        if shape is not None and tuple(t.shape) != shape:
+            raise ValueError(f"{name} has shape {tuple(t.shape)}, not {shape}")
+    if rope_cos is not None and (rope_sin is None or rope_cos.shape != rope_sin.shape or rope_cos.dim() != 2
+                                 or rope_cos.shape[0] < query.shape[0]):
+        raise ValueError("rope_cos and rope_sin must be (query rows, rotated elements) tables of one shape")
     lib = _lib.load()
     out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
     if query.shape[0] == 0:
@@ -110,7 +177,8 @@ def packed_attention(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_
     q_cu, k_cu = q_cu.contiguous(), k_cu.contiguous()
     with torch.cuda.device(query.device):
         args = _args(query, key, value, out, q_cu, k_cu, q_cu.numel() - 1, max_q, scale, window_left, window_right,
-                     spans, plan, plan_split_tiles, key_rows)
+                     spans, plan, plan_split_tiles, key_rows, q_norm, q_norm_eps, q_norm_weight, rope_cos, rope_sin,
+                     gate)
         workspace = None
         if not args.plan_unsplit:
             need = ctypes.c_size_t()
@@ -125,7 +193,7 @@ def packed_attention(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_
 
 @packed_attention.register_fake
 def _(query, key, value, q_cu, k_cu, max_q, scale, window_left, window_right, spans, plan, plan_split_tiles=-1,
-      key_rows=None):
+      key_rows=None, q_norm=0, q_norm_eps=0.0, q_norm_weight=None, rope_cos=None, rope_sin=None, gate=None):
     return query.new_empty(query.shape)
 
 
@@ -191,9 +259,11 @@ def key_rows_of(rows: Tensor | None) -> Tensor | None:
 
 def run(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_cu: Tensor, max_q: int, scale: float,
         window_left: int = -1, window_right: int = -1, spans: Tensor | None = None,
-        plan: Plan | None = None, key_rows: Tensor | None = None) -> Tensor:
+        plan: Plan | None = None, key_rows: Tensor | None = None, q_norm: Norm | None = None,
+        rope: tuple[Tensor, Tensor] | None = None, gate: Tensor | None = None) -> Tensor:
     """``packed_attention`` with a ``Plan`` checked against the call's geometry; ``key_rows`` (int32 or int64) reads
-    the keys and values through a row table instead of a gathered copy."""
+    the keys and values through a row table instead of a gathered copy; ``q_norm`` / ``rope`` ((cos, sin), (rows, R)
+    or (1, rows, R)) the fused query prologue, ``gate`` the fused sigmoid gate on the output."""
     tensor, split_tiles = None, -1
     if plan is not None:
         if (plan.heads, plan.kv_heads, plan.head_dim, plan.window_left, plan.window_right) != (
@@ -203,5 +273,48 @@ def run(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_cu: Tensor, m
                 plan.heads, plan.kv_heads, plan.head_dim, int(max_q)):
             raise ValueError(f"the plan was made for max_q {plan.max_q}, another tile shape than max_q {max_q}")
         tensor, split_tiles = plan.tensor, plan.split_tiles
+    mode, eps, weight = NORM_NONE, 0.0, None
+    if q_norm is not None:
+        mode, eps = int(q_norm.mode), float(q_norm.eps)
+        weight = _bf16_table(q_norm.weight, query.device) if q_norm.weight is not None else None
+    cos = sin = None
+    if rope is not None:
+        cos, sin = (_bf16_table(t, query.device) for t in rope)
     return packed_attention(query, key, value, q_cu, k_cu, int(max_q), float(scale), int(window_left),
-                            int(window_right), spans, tensor, split_tiles, key_rows_of(key_rows))
+                            int(window_right), spans, tensor, split_tiles, key_rows_of(key_rows), mode, eps, weight,
+                            cos, sin, gate)
+
+
+def norm_rope(x: Tensor, norm: Norm | None, rope: tuple[Tensor, Tensor] | None = None,
+              out: Tensor | None = None) -> Tensor:
+    """``x`` (rows, heads, D) bf16 normalised and rotated in one pass over HBM (``karpo_attn_norm_rope``): keys
+    (norm and rotation) and values (norm) for the attention, which stages each key for many query tiles. ``out``
+    may be ``x`` (in place); a new tensor otherwise."""
+    if x.dim() != 3 or x.dtype != torch.bfloat16 or x.device.type != "cuda":
+        raise ValueError("norm_rope takes a (rows, heads, head_dim) bf16 tensor on the GPU")
+    if out is None:
+        out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    elif out.shape != x.shape or out.dtype != x.dtype:
+        raise ValueError("out must have x's shape and dtype")
+    lib = _lib.load()
+    a = _lib.KarpoNormRopeArgs()
+    a.x, a.y = x.data_ptr(), out.data_ptr()
+    a.x_stride_tok, a.x_stride_head = x.stride(0), x.stride(1)
+    a.y_stride_tok, a.y_stride_head = out.stride(0), out.stride(1)
+    a.rows, a.heads, a.head_dim = x.shape[0], x.shape[1], x.shape[2]
+    keep = []
+    if norm is not None:
+        a.norm, a.eps = int(norm.mode), float(norm.eps)
+        if norm.weight is not None:
+            w = _bf16_table(norm.weight, x.device)
+            keep.append(w)
+            a.weight = w.data_ptr()
+    if rope is not None:
+        cos, sin = (_bf16_table(t, x.device) for t in rope)
+        keep += [cos, sin]
+        a.rope_cos, a.rope_sin, a.rope_stride, a.rope_dim = cos.data_ptr(), sin.data_ptr(), cos.stride(0), cos.shape[-1]
+    with torch.cuda.device(x.device):
+        stream = torch.cuda.current_stream(x.device).cuda_stream
+        _lib.check(lib.karpo_attn_norm_rope(ctypes.byref(a), ctypes.c_void_p(stream)), "norm_rope")
+    # converted tables in `keep` go back to the stream-ordered caching allocator after the launch: safe to reuse
+    return out

@@ -14,6 +14,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import types
 
 import numpy as np
 import pytest
@@ -529,3 +530,110 @@ def test_row_table_entries_outside_the_tensor_read_as_zero_keys(gpu):
         got = hip_attention.attend(q, k, v, cu, kc, 64, 0.1, causal=True, rows=rows)
     want = oa.packed_attention(q.cpu(), kz.cpu(), vz.cpu(), [0, 64], [0, 100], 0.1, -1, 0)
     assert_close(got, want, "out-of-range rows")
+
+
+# ---- fused query prologue (norm, rotation) and output gate; keys' and values' norm_rope pass
+
+def _angles(rows: int, r: int, seed: int) -> tuple[torch.Tensor, torch.Tensor]:
+    g = torch.Generator().manual_seed(seed)
+    a = torch.rand(rows, r // 2, generator=g) * 20
+    return torch.cat((a.cos(), a.cos()), -1).bfloat16(), torch.cat((a.sin(), a.sin()), -1).bfloat16()
+
+
+@pytest.mark.parametrize("heads,kv_heads,head", [(32, 16, 128), (16, 8, 256)])
+def test_fused_gemma_query_norm_and_rotation(gpu, heads, kv_heads, head):
+    """The query's Gemma4RMSNorm and rotation (Packed._q, families/gemma/packed.py:191-193) in the kernel's query
+    load: against the oracle applying oracle/prologue.py before the attention, on global and sliding layers."""
+    from oracle import prologue
+
+    torch.manual_seed(14)
+    q_cu = [0, 700, 1500, 1501, 2600]
+    raw = (torch.randn(q_cu[-1], heads, head) * 4).bfloat16()
+    k = torch.randn(q_cu[-1], kv_heads, head).bfloat16()
+    v = torch.randn(q_cu[-1], kv_heads, head).bfloat16()
+    w = (torch.randn(head) * 0.5 + 1).bfloat16()
+    cos, sin = _angles(q_cu[-1], head, 1)
+    q_want = prologue.rope(prologue.rms_norm(raw, prologue.WEIGHT, w, 1e-6), cos, sin)
+    cu = torch.tensor(q_cu, dtype=torch.int32, device=gpu)
+    norm = ops.Norm(ops.NORM_WEIGHT, w.to(gpu), 1e-6)
+    for left, causal, scale in ((-1, True, head ** -0.5), (511, True, head ** -0.5), (-1, False, head ** -0.5),
+                                (-1, True, 1.0)):
+        with torch.inference_mode():
+            got = hip_attention.attend(raw.to(gpu), k.to(gpu), v.to(gpu), cu, cu, 1100, scale, causal=causal,
+                                       window=left, q_norm=norm, cos=cos.to(gpu), sin=sin.to(gpu))
+        want = oa.packed_attention(q_want, k, v, q_cu, q_cu, scale, left, 0 if causal else -1)
+        label = f"gemma prologue {heads}/{kv_heads}/{head} left {left} causal {causal} scale {scale:.3f}"
+        if scale < 1.0:
+            assert_close(got, want, label)
+        else:
+            # Gemma's own scale 1.0 on unit-RMS queries: logits of standard deviation ~sqrt(D), where a last-bit
+            # difference of one rotated query element (fma contraction) moves single outputs by a few 1e-2;
+            # relative criteria, as the reference's large-logit test (tests/gpu/test_triton_attention.py:116-128)
+            diff = (got.float().cpu() - want.float()).abs()
+            rel = float((got.float().cpu() - want.float()).norm() / want.float().norm())
+            print(label, {"max_abs": float(diff.max()), "mean_abs": float(diff.mean()), "rel_fro": rel}, flush=True)
+            assert rel < REL_FRO and float(diff.mean()) <= MEAN_ABS, label
+
+
+@pytest.mark.parametrize("max_q_of", ["pack", "markers"])
+def test_fused_qwen_query_norm_rotation_and_gate(gpu, max_q_of):
+    """Qwen3.5's full-attention layer (families/qwen/packed.py:108-125): the query half of q_proj's output with a
+    Qwen3_5RMSNorm (1 + weight), partial rotation of the first 32 of 128 elements, and sigmoid(gate) on the output,
+    all fused; the pack splits tiles (gate applied by the merge) and the markers-only form runs one-wave tiles."""
+    from oracle import prologue
+
+    torch.manual_seed(15)
+    heads, kv_heads, head = 16, 8, 128
+    lens = [2210, 1547, 1138, 861, 680]
+    cu = _lengths_cu(lens)
+    proj = (torch.randn(cu[-1], heads, 2 * head) * 3).bfloat16()  # q_proj output: (query, gate) halves per head
+    raw, g = proj[..., :head], proj[..., head:]
+    k = torch.randn(cu[-1], kv_heads, head).bfloat16()
+    v = torch.randn(cu[-1], kv_heads, head).bfloat16()
+    w = (torch.randn(head) * 0.2).bfloat16()
+    cos, sin = _angles(cu[-1], 32, 2)
+    if max_q_of == "markers":
+        rows = [b - 1 for b in cu[1:]]
+        raw, g, cos, sin = raw[rows], g[rows], cos[rows], sin[rows]
+        q_cu, window = _lengths_cu([1] * len(lens)), (-1, -1)
+    else:
+        q_cu, window = cu, (-1, 0)
+    q_want = prologue.rope(prologue.rms_norm(raw, prologue.ONE_PLUS, w, 1e-6), cos, sin)
+    want = prologue.gate(oa.packed_attention(q_want, k, v, q_cu, cu, 1 / math.sqrt(head), *window).bfloat16(), g)
+    proj_d = proj.to(gpu) if max_q_of == "pack" else torch.cat((raw, g), -1).to(gpu)
+    qc, kc = (torch.tensor(x, dtype=torch.int32, device=gpu) for x in (q_cu, cu))
+    module = types.SimpleNamespace(weight=w.to(gpu), variance_epsilon=1e-6)
+    with torch.inference_mode():
+        got = varlen.varlen_attn(proj_d[..., :head], k.to(gpu), v.to(gpu), qc, kc, max(b - a for a, b in zip(
+            q_cu[:-1], q_cu[1:])), max(lens), scale=1 / math.sqrt(head), window_size=window, enable_gqa=True,
+            q_norm=module, cos=cos.to(gpu), sin=sin.to(gpu), gate=proj_d[..., head:])
+    assert_close(got, want, f"qwen prologue + gate ({max_q_of})")
+
+
+@pytest.mark.parametrize("head", [64, 128, 256, 512])
+def test_norm_rope_pass_for_keys_and_values(gpu, head):
+    """karpo_attn_norm_rope (the keys' norm and rotation and the values' norm, Packed._kv) against
+    oracle/prologue.py: bf16 results equal but for rare last-bit differences of the reciprocal square root."""
+    from oracle import prologue
+
+    torch.manual_seed(16)
+    x = (torch.randn(333, 4, head) * 5).bfloat16()
+    w = (torch.randn(head) * 0.5 + 1).bfloat16()
+    cases = [(ops.NORM_WEIGHT, w, head), (ops.NORM_ONE_PLUS, w, 32), (ops.NORM_PLAIN, None, None),
+             (ops.NORM_NONE, None, head)]
+    for mode, weight, r in cases:
+        cos, sin = _angles(333, r, 3) if r else (None, None)
+        want = prologue.rms_norm(x, mode, weight, 1e-6) if mode != ops.NORM_NONE else x
+        if r:
+            want = prologue.rope(want, cos, sin)
+        xd = x.to(gpu)
+        norm = ops.Norm(mode, weight.to(gpu) if weight is not None else None, 1e-6)
+        rope = (cos.to(gpu), sin.to(gpu)) if r else None
+        with torch.inference_mode():
+            got = ops.norm_rope(xd, norm, rope).cpu()
+            inplace = ops.norm_rope(xd, norm, rope, out=xd).cpu()
+        assert torch.equal(got, inplace)
+        diff = (got.float() - want.float()).abs()
+        ulp = want.float().abs().clamp_min(1e-30) * 2 ** -7
+        assert (diff <= ulp).all(), (head, mode, float(diff.max()))
+        assert (diff > 0).float().mean() < 1e-2, (head, mode, float((diff > 0).float().mean()))

@@ -133,3 +133,75 @@ def test_a_planted_mask_mistake_is_caught():
     mask = (j <= wrong) & (j >= wrong - 2)
     w = mask / mask.sum(-1, keepdim=True)
     assert not torch.allclose(w.double(), c["want"][:, 0, :lk])
+
+
+# ---- the fused prologue / gate restatement (oracle/prologue.py)
+
+def test_prologue_norms_match_the_transformers_modules():
+    """Gemma4RMSNorm (with and without a weight) and Qwen3_5RMSNorm, the modules the reference's fused norms restate
+    (families/gemma/fused.py:21-25, families/qwen/fused.py:17-19), give the same bf16 values."""
+    from transformers.models.gemma4.modeling_gemma4 import Gemma4RMSNorm
+    from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5RMSNorm
+
+    from oracle import prologue
+
+    torch.manual_seed(21)
+    x = (torch.randn(64, 4, 128) * 3).bfloat16()
+    g = Gemma4RMSNorm(128, eps=1e-6)
+    q = Qwen3_5RMSNorm(128, eps=1e-6)
+    plain = Gemma4RMSNorm(128, eps=1e-6, with_scale=False)
+    with torch.no_grad():
+        g.weight.copy_(torch.randn(128).bfloat16().float())
+        q.weight.copy_((torch.randn(128) * 0.1).bfloat16().float())
+        assert torch.equal(prologue.rms_norm(x, prologue.WEIGHT, g.weight.bfloat16(), 1e-6), g(x))
+        assert torch.equal(prologue.rms_norm(x, prologue.ONE_PLUS, q.weight.bfloat16(), 1e-6), q(x))
+        assert torch.equal(prologue.rms_norm(x, prologue.PLAIN, None, 1e-6), plain(x))
+
+
+def test_prologue_rope_matches_apply_rotary_pos_emb():
+    """Full and partial rotation equal transformers' apply_rotary_pos_emb (the function families/qwen/fused.py:47-48
+    calls) evaluated in float32 and rounded once."""
+    from transformers.models.qwen3_5.modeling_qwen3_5 import apply_rotary_pos_emb
+
+    from oracle import prologue
+
+    torch.manual_seed(22)
+    x = torch.randn(50, 3, 128).bfloat16()
+    for r in (128, 64, 32):
+        angle = torch.randn(50, r // 2)
+        cos = torch.cat((angle.cos(), angle.cos()), -1).bfloat16()
+        sin = torch.cat((angle.sin(), angle.sin()), -1).bfloat16()
+        xf = x.float()[None]  # (batch, rows, heads, D)
+        want, _ = apply_rotary_pos_emb(xf, xf, cos.float()[None], sin.float()[None], unsqueeze_dim=2)
+        assert torch.equal(prologue.rope(x, cos, sin), want[0].bfloat16()), r
+
+
+def test_prologue_closed_forms():
+    from oracle import prologue
+
+    # a constant vector c normalises to c / sqrt(c^2 + eps) times the weight
+    x = torch.full((1, 1, 64), 2.0)
+    out = prologue.rms_norm(x, prologue.WEIGHT, torch.full((64,), 3.0), 0.0)
+    assert torch.allclose(out, torch.full_like(out, 3.0))
+    # without a weight the mean square of the output is 1
+    y = prologue.rms_norm(torch.randn(10, 2, 128) * 7, prologue.PLAIN, None, 0.0)
+    assert torch.allclose(y.pow(2).mean(-1), torch.ones(10, 2), atol=1e-5)
+    # cos 1, sin 0: identity; cos 0, sin 1: the quarter turn (-x2, x1); twice: negation; tail untouched
+    v = torch.randn(4, 2, 128)
+    one, zero = torch.ones(4, 64), torch.zeros(4, 64)
+    assert torch.equal(prologue.rope(v, one, zero), v)
+    turn = prologue.rope(v, zero, one)
+    assert torch.equal(turn[..., :32], -v[..., 32:64]) and torch.equal(turn[..., 32:64], v[..., :32])
+    assert torch.equal(turn[..., 64:], v[..., 64:])
+    assert torch.equal(prologue.rope(turn, zero, one)[..., :64], -v[..., :64])
+    # a rotation keeps each (d, d + R/2) pair's norm
+    a = torch.rand(4, 32) * 6
+    c, s = torch.cat((a.cos(), a.cos()), -1), torch.cat((a.sin(), a.sin()), -1)
+    w = prologue.rope(v, c, s)
+    pair = lambda t: t[..., :32].pow(2) + t[..., 32:64].pow(2)  # noqa: E731
+    assert torch.allclose(pair(w), pair(v), atol=1e-4)
+    # the gate: sigmoid(0) halves, large gates pass or close
+    o = torch.randn(3, 2, 64)
+    assert torch.equal(prologue.gate(o, torch.zeros_like(o)), o * 0.5)
+    assert torch.allclose(prologue.gate(o, torch.full_like(o, 40.0)), o)
+    assert torch.equal(prologue.gate(o, torch.full_like(o, -200.0)), torch.zeros_like(o) * o)
