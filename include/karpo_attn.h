@@ -35,7 +35,7 @@ extern "C" {
 enum {
   KARPO_ATTN_OK = 0,
   KARPO_ATTN_ERR_NULL = 1,        /* a required pointer is NULL */
-  KARPO_ATTN_ERR_HEAD_DIM = 2,    /* head_dim not in {64, 128, 256} */
+  KARPO_ATTN_ERR_HEAD_DIM = 2,    /* head_dim not in {64, 128, 256, 512} */
   KARPO_ATTN_ERR_HEADS = 3,       /* heads or kv_heads < 1, or heads % kv_heads != 0 */
   KARPO_ATTN_ERR_LAYOUT = 4,      /* head_dim not contiguous, a stride not a multiple of 8, or a base not 16-B aligned */
   KARPO_ATTN_ERR_WORKSPACE = 5,   /* workspace NULL or smaller than karpo_attn_workspace_bytes */

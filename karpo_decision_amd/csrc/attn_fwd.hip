@@ -25,7 +25,11 @@
 //   * the running maximum is only raised when a step's maximum exceeds it by more than 2^8 (exact: the final
 //     division by l cancels any common factor), so O is rescaled on few steps;
 //   * a part of a split tile stores its unnormalised fp32 O, running maximum m and sum l; merge_kernel combines the
-//     parts as O = sum_p 2^(m_p - M) O_p / sum_p 2^(m_p - M) l_p with M = max_p m_p.
+//     parts as O = sum_p 2^(m_p - M) O_p / sum_p 2^(m_p - M) l_p with M = max_p m_p;
+//   * at head_dim 512 one wave cannot hold 32 vectors' O (256 fp32 per lane) beside their Q operands, so a pair of
+//     waves shares the vectors, each with half of D: each computes S^T over its half, the pair adds the two partials
+//     through LDS (in the step's K tile, which every wave has finished reading), both run the same softmax, and each
+//     multiplies P into its half of V.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -40,6 +44,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
@@ -53,8 +58,9 @@ constexpr int kBufferFlags = 0x00020000;
 
 // Per head size and tile shape: keys per step (BN) and waves per SIMD the registers are budgeted for (OCC).
 // Wide: D=64 4-wave workgroups, four per CU; D=128 one 12-wave workgroup per CU (three waves per SIMD) sharing one
-// 64-key K/V stream, 64 KiB LDS; D=256 one 8-wave workgroup per CU, 64 KiB LDS. Narrow: one wave per workgroup,
-// 32 KiB LDS (64 KiB at D=256), LDS-limited to five (two) per CU.
+// 64-key K/V stream, 64 KiB LDS; D=256 one 8-wave workgroup per CU, 64 KiB LDS; D=512 one 8-wave workgroup (four
+// pairs, two waves per SIMD), 128 KiB LDS. Narrow: one wave per workgroup (a pair at D=512), 32 KiB LDS (64 KiB at
+// D=256, 128 KiB at D=512), LDS-limited to five (two, one) per CU.
 #ifndef KA_OCC128
 #define KA_OCC128 3
 #endif
@@ -64,7 +70,8 @@ constexpr int kBufferFlags = 0x00020000;
 template <int D, bool NARROW> struct TileCfg {
   static constexpr int W = tile_waves(D, NARROW);
   static constexpr int BN = tile_keys(D, NARROW);
-  static constexpr int OCC = NARROW ? 2 : D == 64 ? 4 : D == 128 ? KA_OCC128 : KA_OCC256;
+  static constexpr int OCC = NARROW ? (D >= 256 ? 1 : 2) : D == 512 ? 2 : D == 64 ? 4 : D == 128 ? KA_OCC128 : KA_OCC256;
+  static constexpr bool PAIR = D == 512;  // a pair of waves per 32 query vectors, each with half of D
 };
 
 // Row of the 32-key block that MFMA A-row r reads: bits 2 and 3 of r swapped.
@@ -145,33 +152,36 @@ __device__ __forceinline__ unsigned pack_bf16(float a, float b) {
 __device__ __forceinline__ float sigmoid(float g) { return 1.f / (1.f + __expf(-g)); }
 
 // Normalised values of 8 consecutive elements d0.. of a query row chunk (bf16-rounded, as the norm's output tensor
-// is), or the raw values when there is no norm; r = rsqrt(mean(q^2) + eps) of the whole vector.
-__device__ __forceinline__ void norm8(const Params& p, const u32x4& raw, int d0, float r, float (&n)[8]) {
-  u32x4 wv = {0, 0, 0, 0};
-  if (p.q_norm == KARPO_NORM_WEIGHT || p.q_norm == KARPO_NORM_ONE_PLUS) wv = *(const u32x4*)(p.q_norm_w + d0);
+// is), or the raw values when there is no norm; r = rsqrt(mean(q^2) + eps) of the whole vector. The weight factor is
+// wm * weight[d] + wa (WEIGHT: 1, 0; ONE_PLUS: 1, 1; PLAIN: 0, 1); without a weight the host points q_norm_w at
+// readable memory, so the code has no per-element branch.
+__device__ __forceinline__ void norm8(const Params& p, const u32x4& raw, int d0, float r, float wm, float wa,
+                                      float (&n)[8]) {
+  const u32x4 wv = *(const u32x4*)(p.q_norm_w + d0);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float h = bf16_at(raw, e);
-    const float w = p.q_norm == KARPO_NORM_WEIGHT ? bf16_at(wv, e)
-                    : p.q_norm == KARPO_NORM_ONE_PLUS ? 1.f + bf16_at(wv, e) : 1.f;
-    n[e] = p.q_norm != KARPO_NORM_NONE ? round_bf16(h * r * w) : h;
-  }
+  for (int e = 0; e < 8; ++e) n[e] = round_bf16(bf16_at(raw, e) * r * __builtin_fmaf(wm, bf16_at(wv, e), wa));
 }
 
-// The query prologue on one lane's half of a query vector (x[dc] holds elements dc*16 + half*8 .. +8 of the row at
-// `row`, pack row `qrow`): RMSNorm over the whole vector (the other half is in the lane 32 away), then rotation by
-// halves of the first rope_dim elements. A rotation partner is read again from the row (same lane, no exchange).
-template <int D>
-__device__ __forceinline__ void query_prologue(const Params& p, const uint16_t* row, int64_t qrow, int half,
-                                            u32x4 (&x)[D / 16]) {
+// The query prologue on chunks c0 .. c0 + NC of one lane's half of a query vector (x[i] holds elements
+// (c0 + i) * 16 + half * 8 .. +8 of the row at `row`, pack row `qrow`): RMSNorm over the whole vector (the sum of
+// squares streams over the row's chunks; the lane 32 away holds the other half), then rotation by halves of the first
+// rope_dim elements. A rotation partner is re-read from the row (same lane, no exchange).
+template <int D, int NC>
+__device__ __forceinline__ void query_prologue(const Params& p, const uint16_t* row, int64_t qrow, int half, int c0,
+                                               u32x4 (&x)[NC]) {
   constexpr int DC = D / 16;
+  const bool norm = p.q_norm != KARPO_NORM_NONE;
+  const float wm = (p.q_norm == KARPO_NORM_WEIGHT || p.q_norm == KARPO_NORM_ONE_PLUS) ? 1.f : 0.f;
+  const float wa = (p.q_norm == KARPO_NORM_ONE_PLUS || p.q_norm == KARPO_NORM_PLAIN) ? 1.f : 0.f;
   float r = 1.f;
-  if (p.q_norm != KARPO_NORM_NONE) {
+  if (norm) {
     float ss = 0.f;
 #pragma unroll
-    for (int dc = 0; dc < DC; ++dc)
+    for (int dc = 0; dc < DC; ++dc) {
+      const u32x4 v = *(const u32x4*)(row + dc * 16 + half * 8);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(bf16_at(x[dc], e), bf16_at(x[dc], e), ss);
+      for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(bf16_at(v, e), bf16_at(v, e), ss);
+    }
     r = 1.f / __builtin_sqrtf(half_swap_sum(ss) * (1.f / D) + p.q_eps);
   }
   // chunk by chunk: a rotation partner is re-read from the row, so no chunk waits on another's registers
@@ -179,20 +189,32 @@ __device__ __forceinline__ void query_prologue(const Params& p, const uint16_t* 
   const uint16_t* cr = p.rope_cos != nullptr ? p.rope_cos + qrow * p.rope_stride : nullptr;
   const uint16_t* sr = p.rope_sin != nullptr ? p.rope_sin + qrow * p.rope_stride : nullptr;
 #pragma unroll
-  for (int dc = 0; dc < DC; ++dc) {
-    const int d0 = dc * 16 + half * 8;
+  for (int i = 0; i < NC; ++i) {
+    const int d0 = (c0 + i) * 16 + half * 8;
     float n[8];
-    norm8(p, x[dc], d0, r, n);
+    if (norm) {
+      norm8(p, x[i], d0, r, wm, wa, n);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) n[e] = bf16_at(x[i], e);
+    }
     if (cr != nullptr && d0 < p.rope_dim) {
       const int dp = d0 < rh ? d0 + rh : d0 - rh;
+      const u32x4 praw = *(const u32x4*)(row + dp);
       float pn[8];
-      norm8(p, *(const u32x4*)(row + dp), dp, r, pn);
-      const u32x4 cv = *(const u32x4*)(cr + d0), sv = *(const u32x4*)(sr + d0);
+      if (norm) {
+        norm8(p, praw, dp, r, wm, wa, pn);
+      } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) n[e] = n[e] * bf16_at(cv, e) + (d0 < rh ? -pn[e] : pn[e]) * bf16_at(sv, e);
+        for (int e = 0; e < 8; ++e) pn[e] = bf16_at(praw, e);
+      }
+      const u32x4 cv = *(const u32x4*)(cr + d0), sv = *(const u32x4*)(sr + d0);
+      const float sgn = d0 < rh ? -1.f : 1.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) n[e] = n[e] * bf16_at(cv, e) + sgn * pn[e] * bf16_at(sv, e);
     }
 #pragma unroll
-    for (int t = 0; t < 4; ++t) x[dc][t] = pack_bf16(n[2 * t], n[2 * t + 1]);
+    for (int t = 0; t < 4; ++t) x[i][t] = pack_bf16(n[2 * t], n[2 * t + 1]);
   }
 }
 
@@ -217,8 +239,11 @@ template <int D, bool NARROW, bool GATHER>
 __global__ __launch_bounds__((64 * TileCfg<D, NARROW>::W), (TileCfg<D, NARROW>::OCC)) void attn_fwd_kernel(Params p) {
   constexpr int W = TileCfg<D, NARROW>::W;  // waves of the workgroup
   constexpr int BN = TileCfg<D, NARROW>::BN;
+  constexpr bool PAIR = TileCfg<D, NARROW>::PAIR;
   constexpr int DC = D / 16;       // 16-wide head-dim chunks of the QK^T contraction
   constexpr int DB = D / 32;       // 32-row head-dim blocks of O^T
+  constexpr int QC = PAIR ? DC / 2 : DC;  // chunks of Q this wave holds (half of D in a pair)
+  constexpr int OB = PAIR ? DB / 2 : DB;  // blocks of O^T this wave accumulates
   constexpr int KB = BN / 32;      // 32-key blocks of S^T
   constexpr int KC = BN / 16;      // 16-key chunks of the PV contraction
   constexpr int TILE = BN * D * 2;  // bytes of one K or V tile
@@ -254,9 +279,10 @@ __global__ __launch_bounds__((64 * TileCfg<D, NARROW>::W), (TileCfg<D, NARROW>::
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 31, half = lane >> 5;
+  const int dh = PAIR ? (wave & 1) : 0;  // in a pair: which half of D this wave holds
 
   // ---- this lane's query vector: position, head, visible key ranges
-  const int vec = wave * 32 + col;
+  const int vec = (PAIR ? (wave >> 1) : wave) * 32 + col;
   const int off = vec / p.ng;
   const int pos = tile * rows_per_tile + off;
   const int head = hg * p.ng + (vec - off * p.ng);
@@ -306,20 +332,20 @@ __global__ __launch_bounds__((64 * TileCfg<D, NARROW>::W), (TileCfg<D, NARROW>::
     }
   }
 
-  bf16x8 qop[DC];
-  {
+  bf16x8 qop[QC];
+  {  // this wave's chunks of the query (a pair's second wave: the second half of D)
     const uint16_t* qrow = p.q + (int64_t)(qa + pos) * p.sq_t + (int64_t)head * p.sq_h;
-    u32x4 x[DC];
+    u32x4 x[QC];
 #pragma unroll
-    for (int dc = 0; dc < DC; ++dc) {
-      x[dc] = u32x4{0, 0, 0, 0};
-      if (valid) x[dc] = *(const u32x4*)(qrow + half * 8 + dc * 16);
+    for (int i = 0; i < QC; ++i) {
+      x[i] = u32x4{0, 0, 0, 0};
+      if (valid) x[i] = *(const u32x4*)(qrow + half * 8 + (dh * QC + i) * 16);
     }
     if (p.q_norm != KARPO_NORM_NONE || p.rope_cos != nullptr) {
-      if (valid) query_prologue<D>(p, qrow, (int64_t)(qa + pos), half, x);
+      if (valid) query_prologue<D, QC>(p, qrow, (int64_t)(qa + pos), half, dh * QC, x);
     }
 #pragma unroll
-    for (int dc = 0; dc < DC; ++dc) qop[dc] = __builtin_bit_cast(bf16x8, x[dc] ^ p.qsign);
+    for (int i = 0; i < QC; ++i) qop[i] = __builtin_bit_cast(bf16x8, x[i] ^ p.qsign);
   }
   int klo = wlo, khi = whi;
   if constexpr (W > 1) {
@@ -410,14 +436,15 @@ __global__ __launch_bounds__((64 * TileCfg<D, NARROW>::W), (TileCfg<D, NARROW>::
     copy_v(j0, vt);
   };
 
-  // ---- LDS read bases (per lane) for the MFMA operands
-  const int k_read = k_offset<D>(key_row(col), half);  // + kb * (2 * D/8 * 256) + dc * 512
+  // ---- LDS read bases (per lane) for the MFMA operands (a pair's second wave starts at the second half of D)
+  const int k_read = k_offset<D>(key_row(col), half) + dh * QC * 512;  // + kb * (2 * D/8 * 256) + dc * 512
   const int g = lane >> 4, jl = lane & 15;
-  const int v_read = v_offset<D>(8 * (g >> 1) + (jl >> 2), 16 * (g & 1) + 4 * (jl & 3));  // + kc, rr, db offsets
+  const int v_read =
+      v_offset<D>(8 * (g >> 1) + (jl >> 2), 16 * (g & 1) + 4 * (jl & 3)) + dh * OB * 256;  // + kc, rr, db offsets
 
-  f32x16 acc[DB];
+  f32x16 acc[OB];
 #pragma unroll
-  for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
+  for (int db = 0; db < OB; ++db) acc[db] = f32x16{};
   float m = -INFINITY, l = 0.f;
   const float c = p.c;
   const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
@@ -440,18 +467,50 @@ __global__ __launch_bounds__((64 * TileCfg<D, NARROW>::W), (TileCfg<D, NARROW>::
     const int j0 = j_first + s * BN;
     if (s + 1 < n_steps) copy_step(j0 + BN, kn, vn);
     if (GATHER && s + 2 < n_steps) fetch_rows(j0 + 2 * BN);
-    if (j0 < whi && j0 + BN > wlo) {  // wave-uniform: some query of this wave sees a key of this step
-      f32x16 st[KB];
+    const bool active = j0 < whi && j0 + BN > wlo;  // wave-uniform: some query of this wave sees a key of the step
+    if (PAIR || active) {  // a pair enters together (its barriers), each wave computes only when active
+    f32x16 st[KB];
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) st[kb] = f32x16{};
+    for (int kb = 0; kb < KB; ++kb) st[kb] = f32x16{};
+    if (active) {
 #pragma unroll
-      for (int dc = 0; dc < DC; ++dc) {
+      for (int dc = 0; dc < QC; ++dc) {
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
           const bf16x8 a = *(const KA_LDS bf16x8*)(kt + k_read + kb * (2 * (D / 8) * 256) + dc * 512);
           st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qop[dc], st[kb], 0, 0, 0);
         }
       }
+    }
+    if constexpr (PAIR) {
+      // the pair adds its two partial S^T through LDS: each wave's 16 floats per lane go to its 4 KiB slot of this
+      // step's K tile, which every wave has finished reading at the first barrier (all waves pass both barriers)
+      static_assert(KB == 1 && W * 4096 <= TILE, "one 32-key block per step; the slots fit the K tile");
+      KA_LDS f32x4* slot = (KA_LDS f32x4*)(const_cast<KA_LDS char*>(kt) + wave * 4096) + lane;
+      const KA_LDS f32x4* other = (const KA_LDS f32x4*)(kt + (wave ^ 1) * 4096) + lane;
+      __syncthreads();
+      if (active) {
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4)
+          slot[q4 * 64] = f32x4{st[0][4 * q4], st[0][4 * q4 + 1], st[0][4 * q4 + 2], st[0][4 * q4 + 3]};
+      }
+      __syncthreads();
+      if (active) {
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {  // low half + high half in that order in both waves: equal sums
+          const f32x4 o = other[q4 * 64];
+          const float x0 = dh ? o.x : st[0][4 * q4], y0 = dh ? st[0][4 * q4] : o.x;
+          const float x1 = dh ? o.y : st[0][4 * q4 + 1], y1 = dh ? st[0][4 * q4 + 1] : o.y;
+          const float x2 = dh ? o.z : st[0][4 * q4 + 2], y2 = dh ? st[0][4 * q4 + 2] : o.z;
+          const float x3 = dh ? o.w : st[0][4 * q4 + 3], y3 = dh ? st[0][4 * q4 + 3] : o.w;
+          st[0][4 * q4] = x0 + y0;
+          st[0][4 * q4 + 1] = x1 + y1;
+          st[0][4 * q4 + 2] = x2 + y2;
+          st[0][4 * q4 + 3] = x3 + y3;
+        }
+      }
+    }
+    if (active) {
       if (!(j0 >= wflo && j0 + BN <= wfhi)) {  // some query of this wave does not see every key of the step
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb)
@@ -475,7 +534,7 @@ __global__ __launch_bounds__((64 * TileCfg<D, NARROW>::W), (TileCfg<D, NARROW>::
         m = mn;
         l *= alpha;
 #pragma unroll
-        for (int db = 0; db < DB; ++db) acc[db] *= alpha;
+        for (int db = 0; db < OB; ++db) acc[db] *= alpha;
       }
       const float msub = m == -INFINITY ? 0.f : m;
       bf16x8 pb[KC];
@@ -496,7 +555,7 @@ __global__ __launch_bounds__((64 * TileCfg<D, NARROW>::W), (TileCfg<D, NARROW>::
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc) {
 #pragma unroll
-        for (int db = 0; db < DB; ++db) {
+        for (int db = 0; db < OB; ++db) {
           bf16x4 pv[2];
 #pragma unroll
           for (int rr = 0; rr < 2; ++rr)
@@ -507,6 +566,7 @@ __global__ __launch_bounds__((64 * TileCfg<D, NARROW>::W), (TileCfg<D, NARROW>::
           acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[kc], acc[db], 0, 0, 0);
         }
       }
+    }
     }
     wait_vmcnt<0>();
     __syncthreads();
@@ -521,17 +581,17 @@ __global__ __launch_bounds__((64 * TileCfg<D, NARROW>::W), (TileCfg<D, NARROW>::
   // ---- store: lane (col, half) holds d = db*32 + (j/4)*8 + half*4 + j%4 of its query vector
   const float lt = half_swap_sum(l);
   if (parts > 1) {  // one part of a split tile: unnormalised fp32 O, m and l for merge_kernel
-    constexpr int V = 32 * W;
+    constexpr int V = tile_vectors(D, NARROW);
     float* base = p.partial + ((int64_t)(slot + part) * p.n_hg + hg) * (int64_t)V * (D + 2);
-    float* op = base + (int64_t)vec * D + half * 4;
+    float* op = base + (int64_t)vec * D + dh * (D / 2) + half * 4;
 #pragma unroll
-    for (int db = 0; db < DB; ++db)
+    for (int db = 0; db < OB; ++db)
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
         float4 x = {acc[db][g4 * 4], acc[db][g4 * 4 + 1], acc[db][g4 * 4 + 2], acc[db][g4 * 4 + 3]};
         *(float4*)(op + db * 32 + g4 * 8) = x;
       }
-    if (half == 0) {
+    if (half == 0 && dh == 0) {
       base[V * D + vec] = m;
       base[V * D + V + vec] = lt;
     }
@@ -539,11 +599,12 @@ __global__ __launch_bounds__((64 * TileCfg<D, NARROW>::W), (TileCfg<D, NARROW>::
   }
   const float inv = lt > 0.f ? 1.f / lt : 0.f;
   if (valid) {
-    uint16_t* op = p.o + (int64_t)(qa + pos) * p.so_t + (int64_t)head * p.so_h + half * 4;
-    const uint16_t* gp =
-        p.gate != nullptr ? p.gate + (int64_t)(qa + pos) * p.sg_t + (int64_t)head * p.sg_h + half * 4 : nullptr;
+    uint16_t* op = p.o + (int64_t)(qa + pos) * p.so_t + (int64_t)head * p.so_h + dh * (D / 2) + half * 4;
+    const uint16_t* gp = p.gate != nullptr
+                             ? p.gate + (int64_t)(qa + pos) * p.sg_t + (int64_t)head * p.sg_h + dh * (D / 2) + half * 4
+                             : nullptr;
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
+    for (int db = 0; db < OB; ++db) {
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
         *(u32x2*)(op + db * 32 + g4 * 8) =
@@ -563,7 +624,7 @@ constexpr int kMergeBlocks = 1024;
 
 template <int D, int W>
 __global__ __launch_bounds__(kMergeThreads) void merge_kernel(Params p) {
-  constexpr int V = 32 * W, C4 = D / 4;
+  constexpr int V = 32 * W / (D == 512 ? 2 : 1), C4 = D / 4;
   if (p.plan[5] != W) return;
   const int64_t units = (int64_t)p.plan[4] * p.n_hg * V * C4;
   const int rows_per_tile = p.plan[1];
@@ -859,7 +920,7 @@ static hipError_t launch_attn(const Params& p, int64_t items, int64_t merges, in
                        dim3(64 * TileCfg<D, NARROW>::W), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || merges <= 0) return e;
-  constexpr int64_t per_merge = (int64_t)32 * TileCfg<D, NARROW>::W * (D / 4);  // threads of one head group
+  constexpr int64_t per_merge = (int64_t)tile_vectors(D, NARROW) * (D / 4);  // threads of one head group
   const int64_t blocks = (merges * n_hg * per_merge + kMergeThreads - 1) / kMergeThreads;
   hipLaunchKernelGGL((merge_kernel<D, TileCfg<D, NARROW>::W>), dim3((unsigned)(blocks < kMergeBlocks ? blocks : kMergeBlocks)),
                      dim3(kMergeThreads), 0, stream, p);
@@ -876,6 +937,8 @@ hipError_t launch_forward(const Params& p, int head_dim, const Geometry& g, int6
     case 257: return launch_attn<128, true>(p, items, merges, g.n_hg, stream);
     case 512: return launch_attn<256, false>(p, items, merges, g.n_hg, stream);
     case 513: return launch_attn<256, true>(p, items, merges, g.n_hg, stream);
+    case 1024: return launch_attn<512, false>(p, items, merges, g.n_hg, stream);
+    case 1025: return launch_attn<512, true>(p, items, merges, g.n_hg, stream);
     default: return hipErrorInvalidValue;
   }
 }

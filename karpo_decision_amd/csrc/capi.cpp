@@ -77,7 +77,7 @@ extern "C" const char* karpo_attn_strerror(int status) {
   switch (status) {
     case KARPO_ATTN_OK: return "ok";
     case KARPO_ATTN_ERR_NULL: return "a required pointer is NULL";
-    case KARPO_ATTN_ERR_HEAD_DIM: return "head_dim must be 64, 128 or 256";
+    case KARPO_ATTN_ERR_HEAD_DIM: return "head_dim must be 64, 128, 256 or 512";
     case KARPO_ATTN_ERR_HEADS: return "heads must be a positive multiple of kv_heads";
     case KARPO_ATTN_ERR_LAYOUT:
       return "tensors need a contiguous head dimension, strides that are multiples of 8 elements and 16-byte aligned "
@@ -212,7 +212,8 @@ extern "C" int karpo_attn_fwd(const KarpoAttnArgs* a, void* stream) {
   p.qsign = a->scale < 0.f ? 0x80008000u : 0u;
   p.q_norm = a->q_norm;
   p.q_eps = a->q_norm_eps;
-  p.q_norm_w = static_cast<const uint16_t*>(a->q_norm_weight);
+  // without a weight the kernel still reads (and multiplies by zero) head_dim elements: q's first row stands in
+  p.q_norm_w = a->q_norm_weight != nullptr ? static_cast<const uint16_t*>(a->q_norm_weight) : p.q;
   p.rope_cos = static_cast<const uint16_t*>(a->rope_cos);
   p.rope_sin = static_cast<const uint16_t*>(a->rope_sin);
   p.rope_stride = a->rope_stride;

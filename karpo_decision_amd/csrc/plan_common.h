@@ -8,9 +8,9 @@
 // one query head.
 //
 // Two tile shapes per head size:
-//   * wide (prefill): several waves share one K/V stream (12 at head_dim 128, 8 at 256, 4 at 64);
+//   * wide (prefill): several waves share one K/V stream (12 at head_dim 128, 8 at 256 and 512, 4 at 64);
 //   * narrow (decode-shaped packs, every sequence's queries fit one wave's 32 vectors, e.g. the markers-only layer
-//     with one query per sequence): one wave per workgroup, several workgroups per CU.
+//     with one query per sequence): one wave per workgroup (one pair at head_dim 512), several per CU.
 // A tile whose key steps exceed the pack's per-workgroup share is split into parts over its key steps; each part
 // writes an fp32 partial (O, running max, sum) and a merge kernel combines them. This bounds the critical path of
 // small packs (few long tiles) and gives decode-shaped packs the parallelism of their keys.
@@ -37,14 +37,19 @@ namespace karpo {
 // Waves per workgroup (each holds 32 query vectors of the tile), keys per step and workgroups resident per CU (the
 // register and LDS budget of the kernel), per head size and tile shape.
 KA_HD constexpr int tile_waves(int head_dim, bool narrow) {
-  return narrow ? 1 : head_dim == 128 ? KA_W128 : head_dim == 256 ? KA_W256 : 4;
+  return head_dim == 512 ? (narrow ? 2 : 8) : narrow ? 1 : head_dim == 128 ? KA_W128 : head_dim == 256 ? KA_W256 : 4;
+}
+// Query vectors per tile: 32 per wave, or per pair of waves at head_dim 512 (each wave of a pair holds half of every
+// vector's elements: half of Q's operands and of O's accumulators).
+KA_HD constexpr int tile_vectors(int head_dim, bool narrow) {
+  return 32 * tile_waves(head_dim, narrow) / (head_dim == 512 ? 2 : 1);
 }
 KA_HD constexpr int tile_keys(int head_dim, bool narrow) {
-  return head_dim == 64 ? 64 : head_dim == 256 ? 32 : narrow ? 32 : KA_BN128;
+  return head_dim == 64 ? 64 : head_dim >= 256 ? 32 : narrow ? 32 : KA_BN128;
 }
 KA_HD constexpr int tiles_per_cu(int head_dim, bool narrow) {
-  // narrow: two K and two V tiles of tile_keys x head_dim bf16 per workgroup in 160 KiB of LDS
-  return narrow ? (head_dim == 256 ? 2 : 5) : head_dim == 64 ? 4 : 1;
+  // two K and two V tiles of tile_keys x head_dim bf16 per workgroup in 160 KiB of LDS (narrow: one wave each)
+  return narrow ? (head_dim == 512 ? 1 : head_dim == 256 ? 2 : 5) : head_dim == 64 ? 4 : 1;
 }
 constexpr int kComputeUnits = 256;   // MI355X
 constexpr int kPlanHeader = 8;       // int32 header of a plan (see karpo_attn.h)
@@ -64,13 +69,13 @@ struct Geometry {
   int conc;      // workgroups the GPU runs at once
 };
 
-KA_HD inline bool head_dim_supported(int d) { return d == 64 || d == 128 || d == 256; }
+KA_HD inline bool head_dim_supported(int d) { return d == 64 || d == 128 || d == 256 || d == 512; }
 
 KA_HD inline Geometry geometry_of(int heads, int kv_heads, int head_dim, bool narrow) {
   Geometry g;
   g.narrow = narrow;
   g.waves = tile_waves(head_dim, narrow);
-  g.vectors = 32 * g.waves;
+  g.vectors = tile_vectors(head_dim, narrow);
   g.bn = tile_keys(head_dim, narrow);
   const int group = heads / kv_heads;
   g.ng = (g.vectors % group == 0) ? group : 1;

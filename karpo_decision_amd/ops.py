@@ -73,8 +73,8 @@ def check_inputs(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_cu: 
         raise ValueError(f"key {tuple(key.shape)} and value {tuple(value.shape)} differ")
     if query.shape[2] != key.shape[2]:
         raise ValueError(f"query head_dim {query.shape[2]} != key head_dim {key.shape[2]}")
-    if query.shape[2] not in (64, 128, 256):
-        raise ValueError(f"head_dim must be 64, 128 or 256, not {query.shape[2]}")
+    if query.shape[2] not in (64, 128, 256, 512):
+        raise ValueError(f"head_dim must be 64, 128, 256 or 512, not {query.shape[2]}")
     if key.shape[1] < 1 or query.shape[1] % key.shape[1] != 0:
         raise ValueError(f"{query.shape[1]} query heads are not a multiple of {key.shape[1]} key/value heads")
     for name, t in (("query", query), ("key", key), ("value", value)):

@@ -179,6 +179,14 @@ def gemma_global(length: int = 32768, device="cuda", seed: int = 0) -> Workload:
                     seed=seed)
 
 
+def gemma_global_512(length: int = 32768, device="cuda", seed: int = 0) -> Workload:
+    """Gemma 4 31B's global layer shape: one causal segment, 32 query / 4 KV heads, head_dim 512
+    (families/gemma/packed.py:1-2; tests/gpu/test_triton_attention.py:32), scale 1/sqrt(512)."""
+    q, k, v = make_tensors(length, 32, 4, 512, seed, device)
+    return Workload(f"gemma-global-d512-causal-{length}", q, k, v, [0, length], [0, length], 1 / math.sqrt(512), -1,
+                    0, seed=seed)
+
+
 def branched(device="cuda", seed: int = 0, prompts: int = 4, shared: int = 4096, branches: int = 4,
              branch: int = 512) -> Workload:
     """A block plan's global layer (families/gemma/packed.py:103-151): ``prompts`` prompts, each a ``shared``-token
@@ -255,6 +263,7 @@ def named(name: str, device="cuda", seed: int = 0) -> Workload:
         "sliding": lambda: gemma_sliding(device, seed),
         "global32k": lambda: gemma_global(32768, device, seed),
         "global131k": lambda: gemma_global(131072, device, seed),
+        "global32k_d512": lambda: gemma_global_512(32768, device, seed),
         "multimodal": lambda: mixed_multimodal(device, seed),
         "markers": lambda: markers_only(device, seed),
         "branched": lambda: branched(device, seed),

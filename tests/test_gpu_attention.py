@@ -143,7 +143,7 @@ def test_mixed_multimodal_workload(gpu):
     check_workload(w, rows=rows, groups=[0, 2, 15])
 
 
-@pytest.mark.parametrize("heads,kv_heads,head", [(32, 4, 128), (4, 1, 64), (16, 8, 256)])
+@pytest.mark.parametrize("heads,kv_heads,head", [(32, 4, 128), (4, 1, 64), (16, 8, 256), (32, 4, 512)])
 def test_one_sequence_matches_float32_math(gpu, heads, kv_heads, head):
     torch.manual_seed(0)
     q = (torch.randn(300, heads, head, device=gpu) / 8).bfloat16()
@@ -158,7 +158,7 @@ def test_one_sequence_matches_float32_math(gpu, heads, kv_heads, head):
     assert_close(got, want.cpu(), f"one-sequence {heads}/{kv_heads}/{head}")
 
 
-@pytest.mark.parametrize("heads,kv_heads,head", [(32, 4, 128), (4, 1, 64)])
+@pytest.mark.parametrize("heads,kv_heads,head", [(32, 4, 128), (4, 1, 64), (32, 4, 512)])
 @pytest.mark.parametrize("causal", [False, True])
 def test_branched_varlen_with_an_empty_sequence(gpu, heads, kv_heads, head, causal):
     """A shared block of 1,000 rows and branches of 37 and 120 rows (each over the shared keys, then its own), and
@@ -199,7 +199,7 @@ def test_keys_past_32_bit_offsets(gpu):
     assert_close(got, want, "keys past 2^31 elements")
 
 
-@pytest.mark.parametrize("heads,kv_heads,head", [(32, 16, 128), (4, 1, 64), (16, 8, 256)])
+@pytest.mark.parametrize("heads,kv_heads,head", [(32, 16, 128), (4, 1, 64), (16, 8, 256), (32, 4, 512)])
 def test_repeated_calls_are_bitwise_equal(gpu, heads, kv_heads, head):
     torch.manual_seed(3)
     q = torch.randn(500, heads, head, device=gpu).bfloat16()
@@ -213,7 +213,7 @@ def test_repeated_calls_are_bitwise_equal(gpu, heads, kv_heads, head):
     assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("heads,kv_heads,head", [(32, 4, 128), (4, 1, 64)])
+@pytest.mark.parametrize("heads,kv_heads,head", [(32, 4, 128), (4, 1, 64), (32, 4, 512)])
 def test_large_logits_match_float32_math(gpu, heads, kv_heads, head):
     """Queries and keys without the usual 1/8, at scale 8: logits reach the hundreds, past float32's exp unless the
     kernel subtracts a running maximum (tests/gpu/test_triton_attention.py:116-128)."""
@@ -331,7 +331,7 @@ def _lengths_cu(lengths):
     return cu
 
 
-@pytest.mark.parametrize("heads,kv_heads,head", [(32, 16, 128), (32, 4, 256), (16, 8, 256), (8, 2, 64), (10, 2, 128)])
+@pytest.mark.parametrize("heads,kv_heads,head", [(32, 16, 128), (32, 4, 256), (16, 8, 256), (8, 2, 64), (10, 2, 128), (32, 4, 512)])
 def test_markers_only_layer(gpu, heads, kv_heads, head):
     """The markers-only global layer (families/gemma/packed.py:267-281): one query per virtual sequence over all of
     its keys, bidirectional, max_q = 1, through the reference-shaped hook. One-wave tiles, key steps split across
@@ -476,7 +476,7 @@ def _block_pack(prompts, window):
     return at, q_cu, g_cu, s_cu, g_rows, s_rows, m_cu, markers
 
 
-@pytest.mark.parametrize("heads,kv_heads,head", [(32, 16, 128), (16, 8, 256), (8, 2, 64)])
+@pytest.mark.parametrize("heads,kv_heads,head", [(32, 16, 128), (16, 8, 256), (8, 2, 64), (32, 4, 512)])
 def test_branch_keys_read_through_row_tables(gpu, heads, kv_heads, head):
     """The fused branch gather (families/gemma/packed.py:222-226): global, sliding and markers-only calls over the
     pack's own K/V with g_rows / s_rows equal, bit for bit, the calls on index_select copies, and match the oracle."""

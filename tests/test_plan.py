@@ -60,8 +60,15 @@ def host_plan(q_cu, k_cu, heads, kv_heads, head_dim, left, right, max_q=_lib.LON
 
 
 #: Workgroups one CU runs at once, per (head_dim, one-wave tiles): the register and LDS budgets of the kernels.
-TILES_PER_CU = {(64, False): 4, (128, False): 1, (256, False): 1, (64, True): 5, (128, True): 5, (256, True): 2}
-GEOMETRIES = [(8, 2, 64), (16, 8, 128), (32, 16, 128), (16, 8, 256), (12, 4, 128), (10, 2, 128), (4, 4, 64)]
+TILES_PER_CU = {(64, False): 4, (128, False): 1, (256, False): 1, (512, False): 1, (64, True): 5, (128, True): 5,
+                (256, True): 2, (512, True): 1}
+GEOMETRIES = [(8, 2, 64), (16, 8, 128), (32, 16, 128), (16, 8, 256), (12, 4, 128), (10, 2, 128), (4, 4, 64),
+              (32, 4, 512), (6, 2, 512)]
+
+
+def waves_of(rows, per, head_dim):
+    """Waves of a tile: 32 query vectors per wave, per pair of waves at head_dim 512."""
+    return rows * per // 32 * (2 if head_dim == 512 else 1)
 
 
 def expected_plan(q_cu, k_cu, heads, kv_heads, head_dim, left, right, max_q):
@@ -90,8 +97,8 @@ def test_host_plan_matches_brute_force(q_lens, extra, geom, left, right, short):
     max_q = max(q_lens)
     rows, bn, per, narrow, merges, items = expected_plan(q_cu, k_cu, heads, kv_heads, head_dim, left, right, max_q)
     header, got_merges, got_items = host_plan(q_cu, k_cu, heads, kv_heads, head_dim, left, right, max_q)
-    waves = 1 if narrow else (32 * 0 + rows * per) // 32
-    assert header[:7] == [len(items), rows, bn, per, len(merges), waves, 8 + 4 * len(merges)]
+    assert header[:7] == [len(items), rows, bn, per, len(merges), waves_of(rows, per, head_dim),
+                          8 + 4 * len(merges)]
     assert header[7] == sum(m[2] for m in merges)
     assert got_merges == merges
     assert got_items == items
@@ -107,7 +114,7 @@ def test_split_bound_is_tight_enough():
         q_cu = [0]
         for n in lens:
             q_cu.append(q_cu[-1] + n)
-        for heads, kv, d in ((16, 8, 128), (32, 16, 128), (16, 8, 256), (8, 2, 64)):
+        for heads, kv, d in ((16, 8, 128), (32, 16, 128), (16, 8, 256), (8, 2, 64), (32, 4, 512)):
             header, merges, items = host_plan(q_cu, q_cu, heads, kv, d, -1, 0, max(lens))
             rows, bn, per = _lib.tile_shape(heads, kv, d, max(lens))
             narrow = rows * per == 32
@@ -141,6 +148,10 @@ def test_tile_geometry():
     assert _lib.tile_shape(32, 4, 256, 4) == (4, 32, 8)
     assert _lib.tile_shape(8, 2, 64, 8) == (8, 64, 4)
     assert _lib.tile_shape(10, 2, 128, 32) == (32, 32, 1)
+    # head_dim 512: a pair of waves per 32 vectors, 8 waves (128 vectors) wide, one pair narrow
+    assert _lib.tile_shape(32, 4, 512) == (16, 32, 8)
+    assert _lib.tile_shape(32, 4, 512, 4) == (4, 32, 8)
+    assert _lib.tile_shape(6, 2, 512) == (128, 32, 1)  # a group of 3 does not divide 128 vectors
 
 
 def test_plan_refuses_bad_bounds_and_small_buffers():
