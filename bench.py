@@ -37,7 +37,9 @@ def parse() -> argparse.Namespace:
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--workload", default="global32k",
-                   help="global32k (default), global131k, qwen, sliding, multimodal, markers, tiny")
+                   help="global32k (default), global131k, global32k_d512, qwen, sliding, multimodal, markers, "
+                        "branched, global32k_prologue, qwen_gated, tiny; keys_norm_rope times karpo_attn_norm_rope "
+                        "over the 32k layer's keys instead")
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-repeats", type=int, default=3)
@@ -60,10 +62,15 @@ def cpu_baseline(w, repeats: int) -> dict:
 
     torch.set_num_threads(int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)))
     group = w.heads // w.kv_heads
+    from oracle import prologue as oracle_prologue
+
     key, value = w.gathered()
     q = w.query[:, :group].cpu()
     k = key[:, :1].cpu()
     v = value[:, :1].cpu()
+    weight = w.q_norm[1].cpu() if w.q_norm is not None else None
+    rope = tuple(t.cpu() for t in w.rope) if w.rope is not None else None
+    gate = w.gate[:, :group].cpu() if w.gate is not None else None
     sample_flops = w.flops() * group / w.heads
     best = None
     times_by_dtype = {}
@@ -71,8 +78,15 @@ def cpu_baseline(w, repeats: int) -> dict:
         times = []
         for n in range(repeats + 1):
             t0 = time.perf_counter()
-            oracle_attention.packed_attention(q, k, v, w.q_cu, w.k_cu, w.scale, w.window_left, w.window_right,
-                                              w.spans, dtype=dtype)
+            qe = q
+            if w.q_norm is not None:  # the reference's fused.norm_rope / norm on the CPU, then the attention
+                qe = oracle_prologue.rms_norm(q, w.q_norm[0], weight, w.q_norm[2])
+            if rope is not None:
+                qe = oracle_prologue.rope(qe, *rope)
+            out = oracle_attention.packed_attention(qe, k, v, w.q_cu, w.k_cu, w.scale, w.window_left, w.window_right,
+                                                    w.spans, dtype=dtype)
+            if gate is not None:
+                oracle_prologue.gate(out.to(torch.bfloat16), gate)
             if n:
                 times.append(time.perf_counter() - t0)
         med = statistics.median(times)
@@ -98,6 +112,43 @@ def cpu_baseline(w, repeats: int) -> dict:
     }
 
 
+def keys_norm_rope(args, device) -> int:
+    """karpo_attn_norm_rope over the keys of the 32k global layer (32,768 rows x 16 heads x 128, Gemma4RMSNorm with
+    a weight, rotation of the whole head), in place: HBM-bound (read and write every key once, plus the tables)."""
+    import torch
+
+    from karpo_decision_amd import ops, workloads
+
+    w = workloads.gemma_global(32768, device, args.seed)
+    keys = w.key.clone()
+    weight = torch.ones(w.head_dim, dtype=torch.bfloat16, device=device)
+    rope = workloads.rope_tables(keys.shape[0], w.head_dim, args.seed, device)
+    norm = ops.Norm(ops.NORM_WEIGHT, weight, 1e-6)
+    for _ in range(args.warmup):
+        ops.norm_rope(keys, norm, rope, out=keys)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(device)
+    marks = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    for a, b in marks:
+        a.record(stream)
+        ops.norm_rope(keys, norm, rope, out=keys)
+        b.record(stream)
+    torch.cuda.synchronize()
+    ms = statistics.median(a.elapsed_time(b) for a, b in marks)
+    nbytes = 2 * keys.numel() * 2 + 2 * rope[0].numel() * 2 + weight.numel() * 2
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "karpo_attn_norm_rope over the 32k layer's keys (HBM bytes / s)", "value": round(gbs, 1),
+        "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "keys-norm-rope-32768", "rows": keys.shape[0], "heads": keys.shape[1],
+                   "head_dim": keys.shape[2], "bytes_per_step": nbytes},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None, "kernel": "norm_rope_kernel<128>",
+                     "avg_launch_ms": round(ms, 4)}}), flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -109,6 +160,8 @@ def main() -> int:
     from karpo_decision_amd import _lib, ops, workloads
 
     device = torch.device("cuda", 0)
+    if args.workload == "keys_norm_rope":
+        return keys_norm_rope(args, device)
     w = workloads.named(args.workload, device, args.seed)
     q_cu = torch.tensor(w.q_cu, dtype=torch.int32, device=device)
     k_cu = torch.tensor(w.k_cu, dtype=torch.int32, device=device)
@@ -116,13 +169,21 @@ def main() -> int:
     plan = ops.make_plan(w.q_cu, w.k_cu, w.heads, w.kv_heads, w.head_dim, w.window_left, w.window_right, device)
     rows = (torch.tensor(w.key_rows, dtype=torch.int32, device=device) if w.key_rows is not None else None)
 
+    fused = {}
+    if w.q_norm is not None:
+        fused["q_norm"] = ops.Norm(*w.q_norm)
+    if w.rope is not None:
+        fused["rope"] = w.rope
+    if w.gate is not None:
+        fused["gate"] = w.gate
+
     def step():
         if rows is not None and args.materialize_gather:
             key, value = w.key.index_select(0, rows), w.value.index_select(0, rows)
             return ops.run(w.query, key, value, q_cu, k_cu, w.max_q, w.scale, w.window_left, w.window_right, spans,
-                           plan)
+                           plan, **fused)
         return ops.run(w.query, w.key, w.value, q_cu, k_cu, w.max_q, w.scale, w.window_left, w.window_right, spans,
-                       plan, rows)
+                       plan, rows, **fused)
 
     with torch.inference_mode():
         for _ in range(args.warmup):

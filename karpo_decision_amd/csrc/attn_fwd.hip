@@ -151,70 +151,136 @@ __device__ __forceinline__ unsigned pack_bf16(float a, float b) {
 }
 __device__ __forceinline__ float sigmoid(float g) { return 1.f / (1.f + __expf(-g)); }
 
-// Normalised values of 8 consecutive elements d0.. of a query row chunk (bf16-rounded, as the norm's output tensor
-// is), or the raw values when there is no norm; r = rsqrt(mean(q^2) + eps) of the whole vector. The weight factor is
-// wm * weight[d] + wa (WEIGHT: 1, 0; ONE_PLUS: 1, 1; PLAIN: 0, 1); without a weight the host points q_norm_w at
-// readable memory, so the code has no per-element branch.
-__device__ __forceinline__ void norm8(const Params& p, const u32x4& raw, int d0, float r, float wm, float wa,
-                                      float (&n)[8]) {
-  const u32x4 wv = *(const u32x4*)(p.q_norm_w + d0);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) n[e] = round_bf16(bf16_at(raw, e) * r * __builtin_fmaf(wm, bf16_at(wv, e), wa));
-}
-
 // The query prologue on chunks c0 .. c0 + NC of one lane's half of a query vector (x[i] holds elements
-// (c0 + i) * 16 + half * 8 .. +8 of the row at `row`, pack row `qrow`): RMSNorm over the whole vector (the sum of
-// squares streams over the row's chunks; the lane 32 away holds the other half), then rotation by halves of the first
-// rope_dim elements. A rotation partner is re-read from the row (same lane, no exchange).
+// (c0 + i) * 16 + half * 8 .. +8 of the row at `row`, pack row `qrow`): RMSNorm over the whole vector (the lane 32
+// away holds the other half; in a pair, the other wave's chunks are read from the row), then rotation by halves of
+// the first rope_dim elements, the partner chunk (d +- rope_dim / 2) read again from the row. Branch-free per chunk:
+// every address is clamped in bounds and selects discard what does not apply, so the loads of a group of chunks
+// issue together (one memory latency per group, not per chunk). Without a weight the host points q_norm_w at
+// readable memory; the weight factor is wm * weight[d] + wa (WEIGHT: 1, 0; ONE_PLUS: 1, 1; PLAIN: 0, 1).
 template <int D, int NC>
 __device__ __forceinline__ void query_prologue(const Params& p, const uint16_t* row, int64_t qrow, int half, int c0,
                                                u32x4 (&x)[NC]) {
   constexpr int DC = D / 16;
+  constexpr int G = NC < 2 ? NC : 2;  // chunks per group of loads
   const bool norm = p.q_norm != KARPO_NORM_NONE;
   const float wm = (p.q_norm == KARPO_NORM_WEIGHT || p.q_norm == KARPO_NORM_ONE_PLUS) ? 1.f : 0.f;
   const float wa = (p.q_norm == KARPO_NORM_ONE_PLUS || p.q_norm == KARPO_NORM_PLAIN) ? 1.f : 0.f;
+  const bool rot = p.rope_cos != nullptr;
+  const int rd = rot ? p.rope_dim : 0, rh = rd >> 1;
   float r = 1.f;
   if (norm) {
     float ss = 0.f;
 #pragma unroll
-    for (int dc = 0; dc < DC; ++dc) {
-      const u32x4 v = *(const u32x4*)(row + dc * 16 + half * 8);
+    for (int i = 0; i < NC; ++i)  // this wave's chunks (compile-time indices keep x in registers)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(bf16_at(x[i], e), bf16_at(x[i], e), ss);
+#pragma unroll
+    for (int i = 0; i < DC - NC; ++i) {  // a pair's other half, from the row
+      const u32x4 v = *(const u32x4*)(row + ((c0 == 0 ? NC : 0) + i) * 16 + half * 8);
 #pragma unroll
       for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(bf16_at(v, e), bf16_at(v, e), ss);
     }
     r = 1.f / __builtin_sqrtf(half_swap_sum(ss) * (1.f / D) + p.q_eps);
   }
-  // chunk by chunk: a rotation partner is re-read from the row, so no chunk waits on another's registers
-  const int rh = p.rope_dim >> 1;
-  const uint16_t* cr = p.rope_cos != nullptr ? p.rope_cos + qrow * p.rope_stride : nullptr;
-  const uint16_t* sr = p.rope_sin != nullptr ? p.rope_sin + qrow * p.rope_stride : nullptr;
-#pragma unroll
-  for (int i = 0; i < NC; ++i) {
-    const int d0 = (c0 + i) * 16 + half * 8;
-    float n[8];
-    if (norm) {
-      norm8(p, x[i], d0, r, wm, wa, n);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) n[e] = bf16_at(x[i], e);
+  if constexpr (NC == DC && D <= 128) {  // the whole half-vector in registers (spare ones): rotate in place
+    switch (rd) {
+      case 0: query_prologue_regs<DC, 0>(p, qrow, half, r, wm, wa, norm, x); return;
+      case 32: query_prologue_regs<DC, 2>(p, qrow, half, r, wm, wa, norm, x); return;
+      case 64: if constexpr (DC >= 4) { query_prologue_regs<DC, 4>(p, qrow, half, r, wm, wa, norm, x); return; }
+      break;
+      case 128: if constexpr (DC >= 8) { query_prologue_regs<DC, 8>(p, qrow, half, r, wm, wa, norm, x); return; }
+      break;
+      case 256: if constexpr (DC >= 16) { query_prologue_regs<DC, 16>(p, qrow, half, r, wm, wa, norm, x); return; }
+      break;
+      default: break;  // other widths: the general path below
     }
-    if (cr != nullptr && d0 < p.rope_dim) {
-      const int dp = d0 < rh ? d0 + rh : d0 - rh;
-      const u32x4 praw = *(const u32x4*)(row + dp);
-      float pn[8];
-      if (norm) {
-        norm8(p, praw, dp, r, wm, wa, pn);
-      } else {
+  }
+  const uint16_t* cr = rot ? p.rope_cos + qrow * p.rope_stride : nullptr;
+  const uint16_t* sr = rot ? p.rope_sin + qrow * p.rope_stride : nullptr;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) pn[e] = bf16_at(praw, e);
+  for (int g0 = 0; g0 < NC; g0 += G) {
+    u32x4 wv[G], pw[G], pr[G], cv[G], sv[G];
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      const int d0 = (c0 + g0 + j) * 16 + half * 8;
+      const bool in = d0 < rd;
+      const int dp = in ? (d0 < rh ? d0 + rh : d0 - rh) : d0;
+      wv[j] = *(const u32x4*)(p.q_norm_w + d0);
+      if (rot) {
+        pw[j] = *(const u32x4*)(p.q_norm_w + dp);
+        pr[j] = *(const u32x4*)(row + dp);
+        cv[j] = *(const u32x4*)(cr + (in ? d0 : 0));
+        sv[j] = *(const u32x4*)(sr + (in ? d0 : 0));
       }
-      const u32x4 cv = *(const u32x4*)(cr + d0), sv = *(const u32x4*)(sr + d0);
-      const float sgn = d0 < rh ? -1.f : 1.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) n[e] = n[e] * bf16_at(cv, e) + sgn * pn[e] * bf16_at(sv, e);
     }
 #pragma unroll
-    for (int t = 0; t < 4; ++t) x[i][t] = pack_bf16(n[2 * t], n[2 * t + 1]);
+    for (int j = 0; j < G; ++j) {
+      const int d0 = (c0 + g0 + j) * 16 + half * 8;
+      const bool in = d0 < rd;
+      const float sgn = d0 < rh ? -1.f : 1.f;
+      float n[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float h = bf16_at(x[g0 + j], e);
+        n[e] = norm ? round_bf16(h * r * __builtin_fmaf(wm, bf16_at(wv[j], e), wa)) : h;
+      }
+      if (rot) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float hp = bf16_at(pr[j], e);
+          const float np = norm ? round_bf16(hp * r * __builtin_fmaf(wm, bf16_at(pw[j], e), wa)) : hp;
+          const float y = n[e] * bf16_at(cv[j], e) + sgn * np * bf16_at(sv[j], e);
+          n[e] = in ? y : n[e];
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) x[g0 + j][t] = pack_bf16(n[2 * t], n[2 * t + 1]);
+    }
+  }
+}
+
+// The prologue when one lane holds all of its half-vector (no pair) and the rotated width is RC * 16 elements
+// (compile time): normalise every chunk in place, then rotate chunks i < RC / 2 with i + RC / 2 in registers (the
+// partner of element d is d +- RC * 8, the same position RC / 2 chunks away). No partner loads or recomputed norms.
+template <int DC, int RC>
+__device__ __forceinline__ void query_prologue_regs(const Params& p, int64_t qrow, int half, float r, float wm,
+                                                    float wa, bool norm, u32x4 (&x)[DC]) {
+  if (norm) {
+#pragma unroll
+    for (int i = 0; i < DC; ++i) {
+      const u32x4 wv = *(const u32x4*)(p.q_norm_w + i * 16 + half * 8);
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        x[i][t] = pack_bf16(bf16_at(x[i], 2 * t) * r * __builtin_fmaf(wm, bf16_at(wv, 2 * t), wa),
+                            bf16_at(x[i], 2 * t + 1) * r * __builtin_fmaf(wm, bf16_at(wv, 2 * t + 1), wa));
+    }
+  }
+  if constexpr (RC > 0) {
+    static_assert(RC % 2 == 0 && RC <= DC, "rotate an even number of chunks");
+    const uint16_t* cr = p.rope_cos + qrow * p.rope_stride + half * 8;
+    const uint16_t* sr = p.rope_sin + qrow * p.rope_stride + half * 8;
+#pragma unroll
+    for (int i = 0; i < RC / 2; ++i) {
+      const u32x4 c0 = *(const u32x4*)(cr + i * 16), s0 = *(const u32x4*)(sr + i * 16);
+      const u32x4 c1 = *(const u32x4*)(cr + (i + RC / 2) * 16), s1 = *(const u32x4*)(sr + (i + RC / 2) * 16);
+      u32x4 lo, hi;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        float a[2], b[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int e = 2 * t + u;
+          const float n0 = bf16_at(x[i], e), n1 = bf16_at(x[i + RC / 2], e);
+          a[u] = n0 * bf16_at(c0, e) - n1 * bf16_at(s0, e);
+          b[u] = n1 * bf16_at(c1, e) + n0 * bf16_at(s1, e);
+        }
+        lo[t] = pack_bf16(a[0], a[1]);
+        hi[t] = pack_bf16(b[0], b[1]);
+      }
+      x[i] = lo;
+      x[i + RC / 2] = hi;
+    }
   }
 }
 
@@ -332,8 +398,10 @@ __global__ __launch_bounds__((64 * TileCfg<D, NARROW>::W), (TileCfg<D, NARROW>::
     }
   }
 
+  // this wave's chunks of the query (a pair's second wave: the second half of D), with the prologue applied; loaded
+  // under the first K/V copy's latency (a pair loads them before: its norm also streams the other half's chunks)
   bf16x8 qop[QC];
-  {  // this wave's chunks of the query (a pair's second wave: the second half of D)
+  auto load_q = [&]() {
     const uint16_t* qrow = p.q + (int64_t)(qa + pos) * p.sq_t + (int64_t)head * p.sq_h;
     u32x4 x[QC];
 #pragma unroll
@@ -346,7 +414,8 @@ __global__ __launch_bounds__((64 * TileCfg<D, NARROW>::W), (TileCfg<D, NARROW>::
     }
 #pragma unroll
     for (int i = 0; i < QC; ++i) qop[i] = __builtin_bit_cast(bf16x8, x[i] ^ p.qsign);
-  }
+  };
+  if constexpr (PAIR) load_q();
   int klo = wlo, khi = whi;
   if constexpr (W > 1) {
     __syncthreads();
@@ -459,6 +528,7 @@ __global__ __launch_bounds__((64 * TileCfg<D, NARROW>::W), (TileCfg<D, NARROW>::
     copy_step(j_first, kt0, vt0);
     if (n_steps > 1) fetch_rows(j_first + BN);
   }
+  if constexpr (!PAIR) load_q();
   wait_vmcnt<0>();
   __syncthreads();
 
@@ -832,70 +902,72 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* __res
   }
 }
 
-// ---- karpo_attn_norm_rope: one wave per (row, head) vector, E = D / 64 contiguous elements per lane; the rotation
-// partner comes through the wave's LDS row.
+// ---- karpo_attn_norm_rope: L = D / 8 lanes per (row, head) vector, 8 elements (16 B) per lane, 64 / L vectors per
+// wave; the sum of squares reduces over the vector's lanes, and a rotation partner (d +- rope_dim / 2, a multiple of
+// 16 elements away) comes from lane +- rope_dim / 16 of the same vector by a lane permute.
 constexpr int kNormRopeWaves = 4;
 
 template <int D>
 __global__ __launch_bounds__(64 * kNormRopeWaves) void norm_rope_kernel(NormRopeParams p) {
-  constexpr int E = D / 64;
-  __shared__ float partner[kNormRopeWaves][D];
+  constexpr int L = D / 8, VPW = 64 / L;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int64_t v = (int64_t)blockIdx.x * kNormRopeWaves + wave; v < p.vectors;
-       v += (int64_t)gridDim.x * kNormRopeWaves) {
-    const int64_t row = v / p.heads;
-    const int head = (int)(v - row * p.heads);
-    const uint16_t* xp = p.x + row * p.sx_t + (int64_t)head * p.sx_h + lane * E;
-    float h[E];
+  const int sub = lane / L, l = lane - sub * L, d0 = l * 8;
+  const bool norm = p.norm != KARPO_NORM_NONE;
+  const float wm = (p.norm == KARPO_NORM_WEIGHT || p.norm == KARPO_NORM_ONE_PLUS) ? 1.f : 0.f;
+  const float wa = (p.norm == KARPO_NORM_ONE_PLUS || p.norm == KARPO_NORM_PLAIN) ? 1.f : 0.f;
+  u32x4 wv = {0, 0, 0, 0};
+  if (p.w != nullptr) wv = *(const u32x4*)(p.w + d0);
+  const bool rot = p.cos != nullptr;
+  const int rd = rot ? p.rope_dim : 0, rh = rd >> 1;
+  const bool in = d0 < rd;
+  const int src = sub * L + (in ? (d0 < rh ? l + rh / 8 : l - rh / 8) : l);  // the partner's lane
+  const float sgn = d0 < rh ? -1.f : 1.f;
+  for (int64_t v0 = ((int64_t)blockIdx.x * kNormRopeWaves + wave) * VPW; v0 < p.vectors;
+       v0 += (int64_t)gridDim.x * kNormRopeWaves * VPW) {
+    const int64_t v = v0 + sub;
+    const bool ok = v < p.vectors;
+    const int64_t row = ok ? v / p.heads : 0;
+    const int head = ok ? (int)(v - row * p.heads) : 0;
+    u32x4 x = {0, 0, 0, 0};
+    if (ok) x = *(const u32x4*)(p.x + row * p.sx_t + (int64_t)head * p.sx_h + d0);
+    float n[8];
+    float ss = 0.f;
 #pragma unroll
-    for (int e = 0; e < E; ++e) h[e] = __uint_as_float((unsigned)xp[e] << 16);
-    float r = 1.f;
-    if (p.norm != KARPO_NORM_NONE) {
-      float ss = 0.f;
+    for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(bf16_at(x, e), bf16_at(x, e), ss);
 #pragma unroll
-      for (int e = 0; e < E; ++e) ss = __builtin_fmaf(h[e], h[e], ss);
+    for (int o = L / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+    const float r = norm ? 1.f / __builtin_sqrtf(ss * (1.f / D) + p.eps) : 1.f;
 #pragma unroll
-      for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
-      r = 1.f / __builtin_sqrtf(ss * (1.f / D) + p.eps);
+    for (int e = 0; e < 8; ++e) {
+      const float h = bf16_at(x, e);
+      n[e] = norm ? round_bf16(h * r * __builtin_fmaf(wm, bf16_at(wv, e), wa)) : h;
+    }
+    if (rot) {
+      u32x4 cv = {0, 0, 0, 0}, sv = {0, 0, 0, 0};
+      if (ok && in) {
+        cv = *(const u32x4*)(p.cos + row * p.rope_stride + d0);
+        sv = *(const u32x4*)(p.sin + row * p.rope_stride + d0);
+      }
 #pragma unroll
-      for (int e = 0; e < E; ++e) {
-        const float wv = p.w != nullptr ? __uint_as_float((unsigned)p.w[lane * E + e] << 16) : 0.f;
-        const float w = p.norm == KARPO_NORM_WEIGHT ? wv : p.norm == KARPO_NORM_ONE_PLUS ? 1.f + wv : 1.f;
-        h[e] = round_bf16(h[e] * r * w);
+      for (int e = 0; e < 8; ++e) {
+        const float pn = __shfl(n[e], src);
+        const float y = n[e] * bf16_at(cv, e) + sgn * pn * bf16_at(sv, e);
+        n[e] = in ? y : n[e];
       }
     }
-    if (p.cos != nullptr) {
-      const int rh = p.rope_dim >> 1;
+    if (ok) {
+      u32x4 out;
 #pragma unroll
-      for (int e = 0; e < E; ++e) partner[wave][lane * E + e] = h[e];
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-      float y[E];
-#pragma unroll
-      for (int e = 0; e < E; ++e) {
-        const int d = lane * E + e;
-        y[e] = h[e];
-        if (d < p.rope_dim) {
-          const float c = __uint_as_float((unsigned)p.cos[row * p.rope_stride + d] << 16);
-          const float s = __uint_as_float((unsigned)p.sin[row * p.rope_stride + d] << 16);
-          const float rot = d < rh ? -partner[wave][d + rh] : partner[wave][d - rh];
-          y[e] = h[e] * c + rot * s;
-        }
-      }
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-#pragma unroll
-      for (int e = 0; e < E; ++e) h[e] = y[e];
+      for (int t = 0; t < 4; ++t) out[t] = pack_bf16(n[2 * t], n[2 * t + 1]);
+      *(u32x4*)(p.y + row * p.sy_t + (int64_t)head * p.sy_h + d0) = out;
     }
-    uint16_t* yp = p.y + row * p.sy_t + (int64_t)head * p.sy_h + lane * E;
-#pragma unroll
-    for (int e = 0; e < E; ++e) yp[e] = __builtin_bit_cast(uint16_t, (__bf16)h[e]);
   }
 }
 
 hipError_t launch_norm_rope(const NormRopeParams& p, int head_dim, hipStream_t stream) {
   if (p.vectors <= 0) return hipSuccess;
-  int64_t blocks = (p.vectors + kNormRopeWaves - 1) / kNormRopeWaves;
+  const int64_t per_block = (int64_t)kNormRopeWaves * (64 / (head_dim / 8));
+  int64_t blocks = (p.vectors + per_block - 1) / per_block;
   if (blocks > 8192) blocks = 8192;
   const dim3 grid((unsigned)blocks), block(64 * kNormRopeWaves);
   switch (head_dim) {

@@ -34,6 +34,11 @@ class Workload:
     spans: list[tuple[int, int]] = field(default_factory=list)
     seed: int = 0
     key_rows: list[int] | None = None  # key row r of the pack is row key_rows[r] of key / value (a block plan's gather)
+    # fused query prologue and gate: (mode, weight, eps) of the norm (oracle/prologue.py modes), (cos, sin) rows per
+    # query row, and the gate; the query is then the projection's raw output
+    q_norm: tuple[int, torch.Tensor, float] | None = None
+    rope: tuple[torch.Tensor, torch.Tensor] | None = None
+    gate: torch.Tensor | None = None
 
     @property
     def heads(self) -> int:
@@ -179,6 +184,34 @@ def gemma_global(length: int = 32768, device="cuda", seed: int = 0) -> Workload:
                     seed=seed)
 
 
+def rope_tables(rows: int, rotated: int, seed: int, device) -> tuple[torch.Tensor, torch.Tensor]:
+    """bf16 (rows, rotated) cos / sin tables of rotation-by-halves form (each angle twice), seeded angles."""
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed + 7)
+    angle = torch.rand(rows, rotated // 2, generator=gen, device=device) * 30
+    return (torch.cat((angle.cos(), angle.cos()), -1).bfloat16(), torch.cat((angle.sin(), angle.sin()), -1).bfloat16())
+
+
+def with_prologue(w: Workload, family: str) -> Workload:
+    """``w`` with its layer's query prologue fused: Gemma (RMSNorm times a weight, rotation of the whole head) or
+    Qwen (RMSNorm times 1 + weight, rotation of the first quarter, sigmoid gate on the output); the query becomes an
+    un-normalised projection output (N(0, 3^2))."""
+    gen = torch.Generator(device=w.query.device)
+    gen.manual_seed(w.seed + 11)
+    d = w.head_dim
+    raw = (torch.randn(w.query.shape, generator=gen, device=w.query.device) * 3).bfloat16()
+    weight = (torch.randn(d, generator=gen, device=w.query.device) * 0.2 + (1.0 if family == "gemma" else 0.0))
+    weight = weight.bfloat16()
+    if family == "gemma":
+        return Workload(w.name + "-prologue", raw, w.key, w.value, w.q_cu, w.k_cu, w.scale, w.window_left,
+                        w.window_right, w.spans, w.seed, w.key_rows, (1, weight, 1e-6),
+                        rope_tables(raw.shape[0], d, w.seed, raw.device))
+    gate = (torch.randn(w.query.shape, generator=gen, device=w.query.device) * 2).bfloat16()
+    return Workload(w.name + "-gated", raw, w.key, w.value, w.q_cu, w.k_cu, w.scale, w.window_left, w.window_right,
+                    w.spans, w.seed, w.key_rows, (2, weight, 1e-6), rope_tables(raw.shape[0], d // 4, w.seed,
+                                                                                raw.device), gate)
+
+
 def gemma_global_512(length: int = 32768, device="cuda", seed: int = 0) -> Workload:
     """Gemma 4 31B's global layer shape: one causal segment, 32 query / 4 KV heads, head_dim 512
     (families/gemma/packed.py:1-2; tests/gpu/test_triton_attention.py:32), scale 1/sqrt(512)."""
@@ -267,6 +300,8 @@ def named(name: str, device="cuda", seed: int = 0) -> Workload:
         "multimodal": lambda: mixed_multimodal(device, seed),
         "markers": lambda: markers_only(device, seed),
         "branched": lambda: branched(device, seed),
+        "global32k_prologue": lambda: with_prologue(gemma_global(32768, device, seed), "gemma"),
+        "qwen_gated": lambda: with_prologue(qwen_full(device, seed), "qwen"),
     }
     if name not in table:
         raise ValueError(f"unknown workload {name!r}; one of {sorted(table)}")

@@ -64,25 +64,42 @@ def run_workload(w: workloads.Workload, plan: ops.Plan | None = None, spans_t=No
     if spans_t is None and w.spans:
         spans_t = torch.tensor(w.spans, dtype=torch.int32, device=dev)
     rows = torch.tensor(w.key_rows, dtype=torch.int32, device=dev) if w.key_rows is not None else None
+    fused = {}
+    if w.q_norm is not None:
+        fused["q_norm"] = ops.Norm(*w.q_norm)
+    if w.rope is not None:
+        fused["rope"] = w.rope
+    if w.gate is not None:
+        fused["gate"] = w.gate
     with torch.inference_mode():
         return ops.run(w.query, w.key, w.value, q_cu, k_cu, w.max_q, w.scale, w.window_left, w.window_right,
-                       spans_t, plan, rows)
+                       spans_t, plan, rows, **fused)
 
 
 def check_workload(w: workloads.Workload, rows=None, groups=None, label=""):
     """Kernel vs oracle on ``rows`` (all when None) of the query heads of KV heads ``groups`` (all when None)."""
+    from oracle import prologue
+
     got = run_workload(w)
     torch.cuda.synchronize()
-    q, (k, v) = w.query, w.gathered()
+    q, (k, v), gate = w.query.cpu(), w.gathered(), w.gate
+    if w.q_norm is not None:  # the layer's query prologue on the CPU first
+        q = prologue.rms_norm(q, w.q_norm[0], w.q_norm[1].cpu(), w.q_norm[2])
+    if w.rope is not None:
+        q = prologue.rope(q, *(t.cpu() for t in w.rope))
     if groups is not None:
         g = w.heads // w.kv_heads
         heads = [kv * g + i for kv in groups for i in range(g)]
         q, k, v = q[:, heads], k[:, groups], v[:, groups]
         got = got[:, heads]
-    want = oa.packed_attention(q.cpu(), k.cpu(), v.cpu(), w.q_cu, w.k_cu, w.scale, w.window_left, w.window_right,
+        gate = gate[:, heads] if gate is not None else None
+    want = oa.packed_attention(q, k.cpu(), v.cpu(), w.q_cu, w.k_cu, w.scale, w.window_left, w.window_right,
                                w.spans, dtype=torch.float32, rows=rows)
     if rows is not None:
         got = got[torch.tensor(rows, device=got.device)]
+        gate = gate[torch.tensor(rows, device=gate.device)] if gate is not None else None
+    if gate is not None:  # the output gate on the bf16 output, as the reference's sigmoid_mul
+        want = prologue.gate(want.bfloat16(), gate.cpu())
     return assert_close(got, want, label or w.name)
 
 
@@ -129,6 +146,16 @@ def test_gemma_sliding_workload_unit_scale(gpu):
 def test_gemma_global_workload(gpu, length):
     w = workloads.gemma_global(length, gpu)
     check_workload(w, rows=sample_rows(w.q_cu, 384, 3), groups=[0, 15])
+
+
+def test_global_layer_with_fused_query_prologue(gpu):
+    w = workloads.with_prologue(workloads.gemma_global(32768, gpu), "gemma")
+    check_workload(w, rows=sample_rows(w.q_cu, 256, seed=7), groups=[3])
+
+
+def test_qwen_layer_with_fused_prologue_and_gate(gpu):
+    w = workloads.with_prologue(workloads.qwen_full(gpu), "qwen")
+    check_workload(w, rows=sample_rows(w.q_cu, 96, seed=8), groups=[0, 7])
 
 
 def test_branched_workload(gpu):
