@@ -239,7 +239,7 @@ def main() -> int:
                    "tokens_per_s": round(w.tokens / (ms_per_step * 1e-3)), "flops_per_step": flops,
                    "min_hbm_bytes_per_step": w.bytes(), "parallelism": "single GPU"},
         "roofline": {**roof, "traffic": traffic,
-                     "kernel": f"attn_fwd_kernel<{w.head_dim}, {str(narrow).lower()}>",
+                     "kernel": f"attn_fwd_kernel<{w.head_dim}, {str(narrow).lower()}, {str(rows is not None).lower()}>",
                      "avg_launch_ms": round(launch_ms, 4)},
     }
     if not args.no_cpu_baseline:
