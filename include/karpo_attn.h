@@ -104,6 +104,11 @@ typedef struct KarpoAttnArgs {
    * o = bf16(bf16(o) * sigmoid(gate)) in fp32. */
   const void* gate;             /* device bf16 [total_q][heads][head_dim] with the strides below, or NULL */
   int64_t gate_stride_tok, gate_stride_head;
+
+  /* Log-sum-exp output for a backward pass (the reference's return_lse, families/gemma/sliding_attention.py:39-41):
+   * lse[h * total_q + row] = ln(sum over the row's visible keys of exp(scale * q.k)), -inf for a row that sees none.
+   * Not with a gate (the gate's own gradient is not this library's). */
+  float* lse;                   /* device fp32 [heads][total_q], or NULL */
 } KarpoAttnArgs;
 
 /* Query / key normalisations of the fused prologue and of karpo_attn_norm_rope. */
@@ -134,6 +139,29 @@ typedef struct KarpoNormRopeArgs {
 } KarpoNormRopeArgs;
 
 int karpo_attn_norm_rope(const KarpoNormRopeArgs* args, void* stream);
+
+/* The backward pass of karpo_attn_fwd (the reference's backward ops: families/gemma/sliding_attention.py:50-61,
+ * families/gemma/global_attention.py:107-118): from the output gradient d_o, the forward's output o and its lse,
+ * d_q = scale * dS K, d_k = scale * dS^T Q (summed over each key/value head's query heads), d_v = P^T d_o, with
+ * P = exp(scale * q.k - lse) over the visible keys and dS = P * (d_o . v - rowsum(d_o * o)). Head sizes 64, 128 and
+ * 256; no plan, no row table, no prologue or gate in fwd (their gradients are other ops'). Gradient tensors are bf16
+ * with head_dim contiguous; every element of d_q, d_k and d_v is written. */
+typedef struct KarpoAttnBwdArgs {
+  KarpoAttnArgs fwd;            /* the forward call's arguments (o = its output); fwd.total_k = rows of k and v;
+                                   fwd.workspace / workspace_bytes: karpo_attn_bwd_workspace_bytes of these args */
+  const void* d_o;              /* device bf16 [total_q][heads][head_dim] */
+  int64_t d_o_stride_tok, d_o_stride_head;
+  const float* lse;             /* device fp32 [heads][total_q]: the forward's lse */
+  void* d_q;
+  int64_t d_q_stride_tok, d_q_stride_head;
+  void* d_k;
+  int64_t d_k_stride_tok, d_k_stride_head;
+  void* d_v;
+  int64_t d_v_stride_tok, d_v_stride_head;
+} KarpoAttnBwdArgs;
+
+int karpo_attn_bwd_workspace_bytes(const KarpoAttnBwdArgs* args, size_t* bytes);
+int karpo_attn_bwd(const KarpoAttnBwdArgs* args, void* stream);
 
 /* Bytes of device workspace karpo_attn_fwd needs for these arguments (reads only sizes: heads, kv_heads, head_dim,
  * n_seq, total_q, max_q). It holds the device plan (when args->plan is NULL) and the fp32 partial results of tiles

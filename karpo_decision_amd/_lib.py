@@ -11,7 +11,8 @@ LIBRARY = Path(__file__).resolve().parent / "libkarpo_attn.so"
 
 #: Every symbol ``include/karpo_attn.h`` declares.
 EXPORTS = ("karpo_attn_fwd", "karpo_attn_plan", "karpo_attn_plan_capacity", "karpo_attn_workspace_bytes",
-           "karpo_attn_tile_shape", "karpo_attn_strerror", "karpo_attn_version", "karpo_attn_norm_rope")
+           "karpo_attn_tile_shape", "karpo_attn_strerror", "karpo_attn_version", "karpo_attn_norm_rope",
+           "karpo_attn_bwd_workspace_bytes", "karpo_attn_bwd")
 
 OK = 0
 ERR_HEAD_DIM, ERR_HEADS, ERR_LAYOUT, ERR_WINDOW, ERR_SPANS, ERR_ARG, ERR_BOUNDS = 2, 3, 4, 6, 7, 9, 11
@@ -39,7 +40,7 @@ class KarpoAttnArgs(ctypes.Structure):
         ("q_norm", ctypes.c_int32), ("q_norm_eps", ctypes.c_float), ("q_norm_weight", ctypes.c_void_p),
         ("rope_cos", ctypes.c_void_p), ("rope_sin", ctypes.c_void_p), ("rope_stride", ctypes.c_int64),
         ("rope_dim", ctypes.c_int32), ("gate", ctypes.c_void_p), ("gate_stride_tok", ctypes.c_int64),
-        ("gate_stride_head", ctypes.c_int64),
+        ("gate_stride_head", ctypes.c_int64), ("lse", ctypes.c_void_p),
     ]
 
 
@@ -52,6 +53,17 @@ class KarpoNormRopeArgs(ctypes.Structure):
         ("norm", ctypes.c_int32), ("eps", ctypes.c_float), ("weight", ctypes.c_void_p),
         ("rope_cos", ctypes.c_void_p), ("rope_sin", ctypes.c_void_p), ("rope_stride", ctypes.c_int64),
         ("rope_dim", ctypes.c_int32),
+    ]
+
+
+class KarpoAttnBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("fwd", KarpoAttnArgs),
+        ("d_o", ctypes.c_void_p), ("d_o_stride_tok", ctypes.c_int64), ("d_o_stride_head", ctypes.c_int64),
+        ("lse", ctypes.c_void_p),
+        ("d_q", ctypes.c_void_p), ("d_q_stride_tok", ctypes.c_int64), ("d_q_stride_head", ctypes.c_int64),
+        ("d_k", ctypes.c_void_p), ("d_k_stride_tok", ctypes.c_int64), ("d_k_stride_head", ctypes.c_int64),
+        ("d_v", ctypes.c_void_p), ("d_v_stride_tok", ctypes.c_int64), ("d_v_stride_head", ctypes.c_int64),
     ]
 
 
@@ -88,6 +100,10 @@ def load() -> ctypes.CDLL:
         lib.karpo_attn_version.restype = ctypes.c_int
         lib.karpo_attn_norm_rope.argtypes = [P(KarpoNormRopeArgs), ctypes.c_void_p]
         lib.karpo_attn_norm_rope.restype = ctypes.c_int
+        lib.karpo_attn_bwd_workspace_bytes.argtypes = [P(KarpoAttnBwdArgs), P(ctypes.c_size_t)]
+        lib.karpo_attn_bwd_workspace_bytes.restype = ctypes.c_int
+        lib.karpo_attn_bwd.argtypes = [P(KarpoAttnBwdArgs), ctypes.c_void_p]
+        lib.karpo_attn_bwd.restype = ctypes.c_int
         _lib = lib
         return lib
 

@@ -1,0 +1,617 @@
+// Packed varlen attention backward for gfx950 (MI355X): bf16 MFMA, fp32 accumulation, the forward's masks.
+//
+// Arithmetic (the textbook flash-attention backward the reference's FA4 / cuDNN backward ops compute,
+// families/gemma/sliding_attention.py:50-61, families/gemma/global_attention.py:107-118): with t = scale * q.k over a
+// query row's visible keys, P = exp(t - lse) (the forward's log-sum-exp), D = rowsum(dO * O),
+//   dV = P^T dO,  dP = dO V^T,  dS = P * (dP - D),  dQ = scale * dS K,  dK = scale * dS^T Q.
+// P and dS enter the MFMAs as bf16 (as P does in the forward), every product accumulates in fp32.
+//
+// Three kernels after the two planners (plan_kernel of attn_fwd.hip, no split tiles):
+//   * bwd_stats_kernel: per (head, query row) the log2-domain LSE (+inf for a row that sees no key, so its P are 0)
+//     and D;
+//   * bwd_dq_kernel (query-stationary, the forward's tiles): Q and dO of 32 query vectors per wave as MFMA B operands
+//     in registers, K and V streamed through LDS; S^T = K Q^T and dP^T = V dO^T with K and V read as row operands
+//     (K layout), dQ^T += K^T dS^T with K read transposed (V layout), so K is staged in both layouts;
+//   * bwd_dkdv_kernel (key-stationary, tiles of 128 keys, four waves of 32): K and V of the wave's keys in registers,
+//     the query rows that see the tile streamed in steps of 32 rows of one head (every head of the GQA group in turn,
+//     which sums the group's gradients): S = Q K^T and dP = dO V^T with Q and dO as row operands, dV^T += dO^T P and
+//     dK^T += Q^T dS with Q and dO read transposed, so Q and dO are staged in both layouts.
+// Rows of a product's row operand are fed in the order that swaps bits 2 and 3 of the row index (key_row), so each
+// lane's 8 consecutive result registers are 8 consecutive rows: P, dS (S^T layout) are directly the B operands of the
+// next products, as in the forward.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "internal.h"
+#include "karpo_attn.h"
+#include "mfma_common.h"
+#include "plan_common.h"
+
+namespace karpo {
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+template <int D> struct BwdCfg {
+  static constexpr int OCC_Q = D >= 256 ? 1 : 2;  // waves per SIMD the registers are budgeted for
+  static constexpr int OCC_K = 1;
+};
+
+// Row (within a 32-row step) of result register j of a lane in half `half` (row operands fed in key_row order).
+__device__ __forceinline__ int result_row(int j, int half) { return (j >> 3) * 16 + half * 8 + (j & 7); }
+
+// ---- stats: L = D / 8 lanes per (row, head) vector, 8 elements per lane
+template <int D>
+__global__ __launch_bounds__(256) void bwd_stats_kernel(BwdParams p) {
+  constexpr int L = D / 8, VPW = 64 / L;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane / L, l = lane - sub * L;
+  const int64_t vectors = p.total_q * p.heads;
+  for (int64_t v0 = ((int64_t)blockIdx.x * 4 + wave) * VPW; v0 < vectors; v0 += (int64_t)gridDim.x * 4 * VPW) {
+    const int64_t v = v0 + sub;
+    const bool ok = v < vectors;
+    const int64_t row = ok ? v / p.heads : 0;
+    const int head = ok ? (int)(v - row * p.heads) : 0;
+    u32x4 x = {0, 0, 0, 0}, y = {0, 0, 0, 0};
+    if (ok) {
+      x = *(const u32x4*)(p.dout + row * p.sdo_t + (int64_t)head * p.sdo_h + l * 8);
+      y = *(const u32x4*)(p.o + row * p.so_t + (int64_t)head * p.so_h + l * 8);
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s = __builtin_fmaf(bf16_at(x, e), bf16_at(y, e), s);
+#pragma unroll
+    for (int o = L / 2; o > 0; o >>= 1) s += __shfl_xor(s, o);
+    if (ok && l == 0) {
+      const float lse = p.lse[(int64_t)head * p.total_q + row];
+      p.stats[((int64_t)head * 2) * p.total_q + row] = lse == -INFINITY ? INFINITY : lse * kLog2e;
+      p.stats[((int64_t)head * 2 + 1) * p.total_q + row] = s;
+    }
+  }
+}
+
+// ---- dQ: the forward's query tiles (plan items: segment, tile), 32 query vectors per wave
+template <int D>
+__global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::OCC_Q) void bwd_dq_kernel(BwdParams p) {
+  constexpr int W = kBwdWaves, BN = kBwdStep;
+  constexpr int DC = D / 16, DB = D / 32, KC = BN / 16;
+  constexpr int TILE = BN * D * 2, BLKS = TILE / 1024, INSTS = (BLKS + W - 1) / W;
+  __shared__ __attribute__((aligned(1024))) char kk0[TILE];  // K, row-operand layout
+  __shared__ __attribute__((aligned(1024))) char kk1[TILE];
+  __shared__ __attribute__((aligned(1024))) char kv0[TILE];  // K, transposed-read layout
+  __shared__ __attribute__((aligned(1024))) char kv1[TILE];
+  __shared__ __attribute__((aligned(1024))) char vk0[TILE];  // V, row-operand layout
+  __shared__ __attribute__((aligned(1024))) char vk1[TILE];
+  __shared__ int red[2][W];
+
+  if (p.plan[2] != BN || p.plan[5] != W) return;
+  const int item = blockIdx.x / p.n_hg;
+  const int hg = blockIdx.x - item * p.n_hg;
+  if (item >= p.plan[0]) return;
+  const int32_t* entry = p.plan + p.plan[6] + kItemInts * item;
+  const int seg = entry[0], tile = entry[1];
+  const int rows_per_tile = p.plan[1];
+  const int qa = p.q_cu[seg], lq = p.q_cu[seg + 1] - qa;
+  const int ka = p.k_cu[seg], lk = p.k_cu[seg + 1] - ka;
+  const int delta = lk - lq;
+  const int kvh = (hg * p.ng) / p.group;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 31, half = lane >> 5;
+
+  // this lane's query vector and the keys it sees (the forward's rule)
+  const int vec = wave * 32 + col;
+  const int off = vec / p.ng;
+  const int pos = tile * rows_per_tile + off;
+  const int head = hg * p.ng + (vec - off * p.ng);
+  const bool valid = pos < lq;
+  int lo = 0, hi = 0, sl = 0, sh = 0;
+  int wlo = INT32_MAX, whi = INT32_MIN, wflo = INT32_MIN, wfhi = INT32_MAX;
+  if (valid) {
+    const int ip = pos + delta;
+    int a = p.left < 0 ? 0 : max(0, ip - p.left);
+    int b = p.right < 0 ? lk : (int)min((int64_t)lk, (int64_t)ip + p.right + 1);
+    if (b < a) b = a;
+    lo = a;
+    hi = b;
+    wflo = a;
+    wfhi = b;
+    if (a < b) {
+      wlo = a;
+      whi = b;
+    }
+    if (p.n_spans > 0) {
+      const int row = qa + pos;
+      int l0 = 0, l1 = p.n_spans;
+      while (l1 - l0 > 1) {
+        const int mid = (l0 + l1) >> 1;
+        if (p.spans[2 * mid] <= row) l0 = mid; else l1 = mid;
+      }
+      const int s0 = p.spans[2 * l0], s1 = p.spans[2 * l0 + 1];
+      if (s0 <= row && row < s1) {
+        const int x = max(0, s0 - qa + delta), y = min(lk, s1 - qa + delta);
+        if (x < y) {
+          sl = x;
+          sh = y;
+          wlo = min(wlo, x);
+          whi = max(whi, y);
+        }
+      }
+    }
+  }
+  wlo = __builtin_amdgcn_readfirstlane(wave_min(wlo));
+  whi = __builtin_amdgcn_readfirstlane(wave_max(whi));
+  wflo = __builtin_amdgcn_readfirstlane(wave_max(wflo));
+  wfhi = __builtin_amdgcn_readfirstlane(wave_min(wfhi));
+  if (lane == 0) {
+    red[0][wave] = wlo;
+    red[1][wave] = whi;
+  }
+  // Q and dO as B operands (lane: its vector, elements dc*16 + half*8 .. +8), the row's log2 LSE and D
+  bf16x8 qop[DC], dop[DC];
+  float lse2 = INFINITY, dsum = 0.f;
+  {
+    const uint16_t* qp = p.q + (int64_t)(qa + pos) * p.sq_t + (int64_t)head * p.sq_h + half * 8;
+    const uint16_t* op = p.dout + (int64_t)(qa + pos) * p.sdo_t + (int64_t)head * p.sdo_h + half * 8;
+#pragma unroll
+    for (int dc = 0; dc < DC; ++dc) {
+      u32x4 x = {0, 0, 0, 0}, y = {0, 0, 0, 0};
+      if (valid) {
+        x = *(const u32x4*)(qp + dc * 16);
+        y = *(const u32x4*)(op + dc * 16);
+      }
+      qop[dc] = __builtin_bit_cast(bf16x8, x);
+      dop[dc] = __builtin_bit_cast(bf16x8, y);
+    }
+    if (valid) {
+      lse2 = p.stats[((int64_t)head * 2) * p.total_q + qa + pos];
+      dsum = p.stats[((int64_t)head * 2 + 1) * p.total_q + qa + pos];
+    }
+  }
+  __syncthreads();
+  int klo = INT32_MAX, khi = INT32_MIN;
+#pragma unroll
+  for (int w = 0; w < W; ++w) {
+    klo = min(klo, red[0][w]);
+    khi = max(khi, red[1][w]);
+  }
+  klo = __builtin_amdgcn_readfirstlane(klo);
+  khi = __builtin_amdgcn_readfirstlane(khi);
+  const int j_first = klo < khi ? (klo / BN) * BN : 0;
+  const int n_steps = klo < khi ? (khi - j_first + BN - 1) / BN : 0;
+
+  // copies: K into both layouts, V into the row-operand layout (zeros past the sequence's last key)
+  const uint16_t* kbase = p.k + (int64_t)kvh * p.sk_h + (int64_t)ka * p.sk_t;
+  const uint16_t* vbase = p.v + (int64_t)kvh * p.sv_h + (int64_t)ka * p.sv_t;
+  uint32_t kk_off[INSTS], kv_off[INSTS], vk_off[INSTS];
+#pragma unroll
+  for (int r = 0; r < INSTS; ++r) {
+    int key, colm;
+    k_dma_source<D>(wave * INSTS + r, lane, &key, &colm);
+    kk_off[r] = (uint32_t)(key * p.sk_t + colm) * 2u;
+    vk_off[r] = (uint32_t)(key * p.sv_t + colm) * 2u;
+    v_dma_source<D>(wave * INSTS + r, lane, &key, &colm);
+    kv_off[r] = (uint32_t)(key * p.sk_t + colm) * 2u;
+  }
+  auto copy_step = [&](int j0, KA_LDS char* tkk, KA_LDS char* tkv, KA_LDS char* tvk) {
+    const int rows = min(lk - j0, BN);
+    const uint16_t* ks = kbase + (int64_t)j0 * p.sk_t;
+    const uint16_t* vs = vbase + (int64_t)j0 * p.sv_t;
+#pragma unroll
+    for (int r = 0; r < INSTS; ++r)
+      if (BLKS % W == 0 || wave * INSTS + r < BLKS) {
+        const int at = (wave * INSTS + r) * 1024;
+        dma_16b(ks, rows * (int)p.sk_t * 2, tkk + at, kk_off[r]);
+        dma_16b(ks, rows * (int)p.sk_t * 2, tkv + at, kv_off[r]);
+        dma_16b(vs, rows * (int)p.sv_t * 2, tvk + at, vk_off[r]);
+      }
+  };
+  const int k_read = k_offset<D>(key_row(col), half);
+  const int g = lane >> 4, jl = lane & 15;
+  const int v_read = v_offset<D>(8 * (g >> 1) + (jl >> 2), 16 * (g & 1) + 4 * (jl & 3));
+  f32x16 acc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
+  const float c = p.c;
+
+  KA_LDS char* const tkk0 = (KA_LDS char*)kk0;
+  KA_LDS char* const tkk1 = (KA_LDS char*)kk1;
+  KA_LDS char* const tkv0 = (KA_LDS char*)kv0;
+  KA_LDS char* const tkv1 = (KA_LDS char*)kv1;
+  KA_LDS char* const tvk0 = (KA_LDS char*)vk0;
+  KA_LDS char* const tvk1 = (KA_LDS char*)vk1;
+  if (n_steps > 0) copy_step(j_first, tkk0, tkv0, tvk0);
+  wait_vmcnt<0>();
+  __syncthreads();
+
+  auto step = [&](int s, const KA_LDS char* tkk, const KA_LDS char* tkv, const KA_LDS char* tvk, KA_LDS char* nkk,
+                  KA_LDS char* nkv, KA_LDS char* nvk) {
+    const int j0 = j_first + s * BN;
+    if (s + 1 < n_steps) copy_step(j0 + BN, nkk, nkv, nvk);
+    if (j0 < whi && j0 + BN > wlo) {
+      f32x16 st = f32x16{}, dpt = f32x16{};
+#pragma unroll
+      for (int dc = 0; dc < DC; ++dc) {
+        const bf16x8 a = *(const KA_LDS bf16x8*)(tkk + k_read + dc * 512);
+        st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qop[dc], st, 0, 0, 0);
+        const bf16x8 b = *(const KA_LDS bf16x8*)(tvk + k_read + dc * 512);
+        dpt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, dop[dc], dpt, 0, 0, 0);
+      }
+      const bool partial = !(j0 >= wflo && j0 + BN <= wfhi);
+      bf16x8 dsb[KC];
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          const int jj = kc * 8 + t;
+          const int key = j0 + (jj >> 3) * 16 + half * 8 + (jj & 7);
+          const bool vis = !partial || (((unsigned)(key - lo) < (unsigned)(hi - lo)) |
+                                        ((unsigned)(key - sl) < (unsigned)(sh - sl)));
+          const float pr = vis ? __builtin_amdgcn_exp2f(__builtin_fmaf(st[jj], c, -lse2)) : 0.f;
+          dsb[kc][t] = (__bf16)(pr * (dpt[jj] - dsum));
+        }
+      }
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) {
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          bf16x4 pv[2];
+#pragma unroll
+          for (int rr = 0; rr < 2; ++rr)
+            pv[rr] = __builtin_bit_cast(
+                bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                            (KA_LDS s16x4*)(tkv + v_read + (kc * 4 + rr) * (D / 16) * 128 + db * 256)));
+          const bf16x8 a = __builtin_shufflevector(pv[0], pv[1], 0, 1, 2, 3, 4, 5, 6, 7);
+          acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, dsb[kc], acc[db], 0, 0, 0);
+        }
+      }
+    }
+    wait_vmcnt<0>();
+    __syncthreads();
+  };
+  int s = 0;
+  for (; s + 1 < n_steps; s += 2) {
+    step(s, tkk0, tkv0, tvk0, tkk1, tkv1, tvk1);
+    step(s + 1, tkk1, tkv1, tvk1, tkk0, tkv0, tvk0);
+  }
+  if (s < n_steps) step(s, tkk0, tkv0, tvk0, tkk1, tkv1, tvk1);
+
+  if (valid) {  // dq = scale * acc: lane (col, half) holds d = db*32 + (j/4)*8 + half*4 + j%4
+    uint16_t* dp = p.dq + (int64_t)(qa + pos) * p.sdq_t + (int64_t)head * p.sdq_h + half * 4;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        u32x2 w;
+        w[0] = pack_bf16(acc[db][g4 * 4] * p.scale, acc[db][g4 * 4 + 1] * p.scale);
+        w[1] = pack_bf16(acc[db][g4 * 4 + 2] * p.scale, acc[db][g4 * 4 + 3] * p.scale);
+        *(u32x2*)(dp + db * 32 + g4 * 8) = w;
+      }
+  }
+}
+
+// ---- dK, dV: key tiles of 128 (plan items of the bounds swapped: segment, key tile), 32 keys per wave. MODE bit 0:
+// compute dV, bit 1: dK (head size 256 runs the two as separate launches: both accumulators and both operands do not
+// fit one wave's registers).
+template <int D, int MODE>
+__global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::OCC_K) void bwd_dkdv_kernel(BwdParams p) {
+  constexpr bool DV = (MODE & 1) != 0, DK = (MODE & 2) != 0;
+  constexpr int W = kBwdWaves, BQ = kBwdStep;
+  constexpr int DC = D / 16, DB = D / 32, KC = BQ / 16;
+  constexpr int TILE = BQ * D * 2, BLKS = TILE / 1024, INSTS = (BLKS + W - 1) / W;
+  __shared__ __attribute__((aligned(1024))) char qk0[TILE];  // Q, row-operand layout
+  __shared__ __attribute__((aligned(1024))) char qk1[TILE];
+  __shared__ __attribute__((aligned(1024))) char qv0[TILE];  // Q, transposed-read layout
+  __shared__ __attribute__((aligned(1024))) char qv1[TILE];
+  __shared__ __attribute__((aligned(1024))) char ok0[TILE];  // dO, row-operand layout
+  __shared__ __attribute__((aligned(1024))) char ok1[TILE];
+  __shared__ __attribute__((aligned(1024))) char ov0[TILE];  // dO, transposed-read layout
+  __shared__ __attribute__((aligned(1024))) char ov1[TILE];
+  __shared__ __attribute__((aligned(256))) float sts0[2 * BQ];  // log2 LSE, then D, of the step's rows
+  __shared__ __attribute__((aligned(256))) float sts1[2 * BQ];
+  __shared__ int red[2][W];
+
+  if (p.plan[2] != BQ || p.plan[5] != W) return;
+  const int item = blockIdx.x / p.n_hg;
+  const int kvh = blockIdx.x - item * p.n_hg;
+  if (item >= p.plan[0]) return;
+  const int32_t* entry = p.plan + p.plan[6] + kItemInts * item;
+  const int seg = entry[0], ktile = entry[1];
+  const int keys_per_tile = p.plan[1];
+  const int qa = p.q_cu[seg], lq = p.q_cu[seg + 1] - qa;
+  const int ka = p.k_cu[seg], lk = p.k_cu[seg + 1] - ka;
+  const int delta = lk - lq;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 31, half = lane >> 5;
+
+  // this lane's key and the query rows that see it: j - right <= i + delta <= j + left, or both in one span
+  const int key = ktile * keys_per_tile + wave * 32 + col;
+  const bool valid = key < lk;
+  int rlo = 0, rhi = 0, srl = 0, srh = 0;
+  int wlo = INT32_MAX, whi = INT32_MIN, wflo = INT32_MIN, wfhi = INT32_MAX;
+  if (valid) {
+    int a = p.right < 0 ? 0 : max(0, key - p.right - delta);
+    int b = p.left < 0 ? lq : (int)min((int64_t)lq, (int64_t)key + p.left - delta + 1);
+    if (b < a) b = a;
+    rlo = a;
+    rhi = b;
+    wflo = a;
+    wfhi = b;
+    if (a < b) {
+      wlo = a;
+      whi = b;
+    }
+    const int kq = key - delta;  // the key's position in query rows
+    if (p.n_spans > 0 && kq >= 0 && kq < lq) {
+      const int row = qa + kq;
+      int l0 = 0, l1 = p.n_spans;
+      while (l1 - l0 > 1) {
+        const int mid = (l0 + l1) >> 1;
+        if (p.spans[2 * mid] <= row) l0 = mid; else l1 = mid;
+      }
+      const int s0 = p.spans[2 * l0], s1 = p.spans[2 * l0 + 1];
+      if (s0 <= row && row < s1) {
+        const int x = max(0, s0 - qa), y = min(lq, s1 - qa);
+        if (x < y) {
+          srl = x;
+          srh = y;
+          wlo = min(wlo, x);
+          whi = max(whi, y);
+        }
+      }
+    }
+  }
+  wlo = __builtin_amdgcn_readfirstlane(wave_min(wlo));
+  whi = __builtin_amdgcn_readfirstlane(wave_max(whi));
+  wflo = __builtin_amdgcn_readfirstlane(wave_max(wflo));
+  wfhi = __builtin_amdgcn_readfirstlane(wave_min(wfhi));
+  if (lane == 0) {
+    red[0][wave] = wlo;
+    red[1][wave] = whi;
+  }
+  // K and V of the lane's key as B operands (elements dc*16 + half*8 .. +8)
+  bf16x8 kop[DC], vop[DC];
+  {
+    const uint16_t* kp = p.k + (int64_t)(ka + key) * p.sk_t + (int64_t)kvh * p.sk_h + half * 8;
+    const uint16_t* vp = p.v + (int64_t)(ka + key) * p.sv_t + (int64_t)kvh * p.sv_h + half * 8;
+#pragma unroll
+    for (int dc = 0; dc < DC; ++dc) {
+      u32x4 x = {0, 0, 0, 0}, y = {0, 0, 0, 0};
+      if (valid) {
+        x = *(const u32x4*)(kp + dc * 16);
+        if constexpr (DK) y = *(const u32x4*)(vp + dc * 16);
+      }
+      kop[dc] = __builtin_bit_cast(bf16x8, x);
+      if constexpr (DK) vop[dc] = __builtin_bit_cast(bf16x8, y);
+    }
+  }
+  __syncthreads();
+  int qlo = INT32_MAX, qhi = INT32_MIN;
+#pragma unroll
+  for (int w = 0; w < W; ++w) {
+    qlo = min(qlo, red[0][w]);
+    qhi = max(qhi, red[1][w]);
+  }
+  qlo = __builtin_amdgcn_readfirstlane(qlo);
+  qhi = __builtin_amdgcn_readfirstlane(qhi);
+  const int r_first = qlo < qhi ? (qlo / BQ) * BQ : 0;
+  const int n_rsteps = qlo < qhi ? (qhi - r_first + BQ - 1) / BQ : 0;
+  const int n_steps = n_rsteps * p.group;  // every head of the group in turn
+
+  uint32_t qk_off[INSTS], qv_off[INSTS], ok_off[INSTS], ov_off[INSTS];
+#pragma unroll
+  for (int r = 0; r < INSTS; ++r) {
+    int row, colm;
+    k_dma_source<D>(wave * INSTS + r, lane, &row, &colm);
+    qk_off[r] = (uint32_t)(row * p.sq_t + colm) * 2u;
+    ok_off[r] = (uint32_t)(row * p.sdo_t + colm) * 2u;
+    v_dma_source<D>(wave * INSTS + r, lane, &row, &colm);
+    qv_off[r] = (uint32_t)(row * p.sq_t + colm) * 2u;
+    ov_off[r] = (uint32_t)(row * p.sdo_t + colm) * 2u;
+  }
+  // step s: head kvh * group + s / n_rsteps, rows r_first + (s % n_rsteps) * BQ ..
+  auto copy_step = [&](int s, KA_LDS char* tqk, KA_LDS char* tqv, KA_LDS char* tok, KA_LDS char* tov,
+                       KA_LDS float* tst) {
+    const int h = kvh * p.group + s / n_rsteps;
+    const int r0 = r_first + (s % n_rsteps) * BQ;
+    const int rows = min(lq - r0, BQ);
+    const uint16_t* qs = p.q + (int64_t)(qa + r0) * p.sq_t + (int64_t)h * p.sq_h;
+    const uint16_t* os = p.dout + (int64_t)(qa + r0) * p.sdo_t + (int64_t)h * p.sdo_h;
+#pragma unroll
+    for (int r = 0; r < INSTS; ++r)
+      if (BLKS % W == 0 || wave * INSTS + r < BLKS) {
+        const int at = (wave * INSTS + r) * 1024;
+        dma_16b(qs, rows * (int)p.sq_t * 2, tqk + at, qk_off[r]);
+        if constexpr (DK) {
+          dma_16b(qs, rows * (int)p.sq_t * 2, tqv + at, qv_off[r]);
+          dma_16b(os, rows * (int)p.sdo_t * 2, tok + at, ok_off[r]);
+        }
+        if constexpr (DV) dma_16b(os, rows * (int)p.sdo_t * 2, tov + at, ov_off[r]);
+      }
+    if (wave == W - 1) {  // 32 log2 LSE (lanes 0-31) then 32 D (lanes 32-63), 4 B per lane; zeros past the stats
+      const float* src = p.stats + (int64_t)h * 2 * p.total_q + qa + r0;
+      const __amdgpu_buffer_rsrc_t rs =
+          __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, (int)(p.total_q + rows) * 4, kBufferFlags);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (KA_LDS void*)tst, 4,
+                                               (uint32_t)((lane >> 5) * p.total_q + (lane & 31)) * 4u, 0, 0, 0);
+    }
+  };
+  const int q_read = k_offset<D>(key_row(col), half);
+  const int g = lane >> 4, jl = lane & 15;
+  const int v_read = v_offset<D>(8 * (g >> 1) + (jl >> 2), 16 * (g & 1) + 4 * (jl & 3));
+  f32x16 dk[DB], dv[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+    dk[db] = f32x16{};
+    dv[db] = f32x16{};
+  }
+  const float c = p.c;
+
+  KA_LDS char* const tqk0 = (KA_LDS char*)qk0;
+  KA_LDS char* const tqk1 = (KA_LDS char*)qk1;
+  KA_LDS char* const tqv0 = (KA_LDS char*)qv0;
+  KA_LDS char* const tqv1 = (KA_LDS char*)qv1;
+  KA_LDS char* const tok0 = (KA_LDS char*)ok0;
+  KA_LDS char* const tok1 = (KA_LDS char*)ok1;
+  KA_LDS char* const tov0 = (KA_LDS char*)ov0;
+  KA_LDS char* const tov1 = (KA_LDS char*)ov1;
+  KA_LDS float* const tst0 = (KA_LDS float*)sts0;
+  KA_LDS float* const tst1 = (KA_LDS float*)sts1;
+  if (n_steps > 0) copy_step(0, tqk0, tqv0, tok0, tov0, tst0);
+  wait_vmcnt<0>();
+  __syncthreads();
+
+  auto step = [&](int s, const KA_LDS char* tqk, const KA_LDS char* tqv, const KA_LDS char* tok,
+                  const KA_LDS char* tov, const KA_LDS float* tst, KA_LDS char* nqk, KA_LDS char* nqv,
+                  KA_LDS char* nok, KA_LDS char* nov, KA_LDS float* nst) {
+    if (s + 1 < n_steps) copy_step(s + 1, nqk, nqv, nok, nov, nst);
+    const int r0 = r_first + (s % n_rsteps) * BQ;
+    if (r0 < whi && r0 + BQ > wlo) {
+      f32x16 st = f32x16{}, dpt = f32x16{};
+#pragma unroll
+      for (int dc = 0; dc < DC; ++dc) {
+        const bf16x8 a = *(const KA_LDS bf16x8*)(tqk + q_read + dc * 512);
+        st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, kop[dc], st, 0, 0, 0);
+        if constexpr (DK) {
+          const bf16x8 b = *(const KA_LDS bf16x8*)(tok + q_read + dc * 512);
+          dpt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, vop[dc], dpt, 0, 0, 0);
+        }
+      }
+      // the step rows' log2 LSE and D for this lane's result registers (rows half*8 .. and 16 + half*8 ..)
+      f32x4 ls[4], ds[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int r = (u >> 1) * 16 + half * 8 + (u & 1) * 4;
+        ls[u] = *(const KA_LDS f32x4*)(tst + r);
+        ds[u] = *(const KA_LDS f32x4*)(tst + BQ + r);
+      }
+      const bool partial = !(r0 >= wflo && r0 + BQ <= wfhi);
+      bf16x8 pb[KC], dsb[KC];
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          const int jj = kc * 8 + t;
+          const int row = r0 + result_row(jj, half);
+          const bool vis = !partial || (((unsigned)(row - rlo) < (unsigned)(rhi - rlo)) |
+                                        ((unsigned)(row - srl) < (unsigned)(srh - srl)));
+          const float l2 = ls[jj >> 2][jj & 3], dd = ds[jj >> 2][jj & 3];
+          const float pr = vis ? __builtin_amdgcn_exp2f(__builtin_fmaf(st[jj], c, -l2)) : 0.f;
+          if constexpr (DV) pb[kc][t] = (__bf16)pr;
+          if constexpr (DK) dsb[kc][t] = (__bf16)(pr * (dpt[jj] - dd));
+        }
+      }
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) {
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          bf16x4 ov[2], qv[2];
+#pragma unroll
+          for (int rr = 0; rr < 2; ++rr) {
+            const int at = v_read + (kc * 4 + rr) * (D / 16) * 128 + db * 256;
+            if constexpr (DV)
+              ov[rr] = __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((KA_LDS s16x4*)(tov + at)));
+            if constexpr (DK)
+              qv[rr] = __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((KA_LDS s16x4*)(tqv + at)));
+          }
+          if constexpr (DV) {
+            const bf16x8 ao = __builtin_shufflevector(ov[0], ov[1], 0, 1, 2, 3, 4, 5, 6, 7);
+            dv[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ao, pb[kc], dv[db], 0, 0, 0);
+          }
+          if constexpr (DK) {
+            const bf16x8 aq = __builtin_shufflevector(qv[0], qv[1], 0, 1, 2, 3, 4, 5, 6, 7);
+            dk[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aq, dsb[kc], dk[db], 0, 0, 0);
+          }
+        }
+      }
+    }
+    wait_vmcnt<0>();
+    __syncthreads();
+  };
+  int s = 0;
+  for (; s + 1 < n_steps; s += 2) {
+    step(s, tqk0, tqv0, tok0, tov0, tst0, tqk1, tqv1, tok1, tov1, tst1);
+    step(s + 1, tqk1, tqv1, tok1, tov1, tst1, tqk0, tqv0, tok0, tov0, tst0);
+  }
+  if (s < n_steps) step(s, tqk0, tqv0, tok0, tov0, tst0, tqk1, tqv1, tok1, tov1, tst1);
+
+  if (valid) {  // lane (col, half) holds d = db*32 + (j/4)*8 + half*4 + j%4 of its key
+    uint16_t* kq = p.dk + (int64_t)(ka + key) * p.sdk_t + (int64_t)kvh * p.sdk_h + half * 4;
+    uint16_t* vq = p.dv + (int64_t)(ka + key) * p.sdv_t + (int64_t)kvh * p.sdv_h + half * 4;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        if constexpr (DK) {
+          u32x2 a;
+          a[0] = pack_bf16(dk[db][g4 * 4] * p.scale, dk[db][g4 * 4 + 1] * p.scale);
+          a[1] = pack_bf16(dk[db][g4 * 4 + 2] * p.scale, dk[db][g4 * 4 + 3] * p.scale);
+          *(u32x2*)(kq + db * 32 + g4 * 8) = a;
+        }
+        if constexpr (DV) {
+          u32x2 b;
+          b[0] = pack_bf16(dv[db][g4 * 4], dv[db][g4 * 4 + 1]);
+          b[1] = pack_bf16(dv[db][g4 * 4 + 2], dv[db][g4 * 4 + 3]);
+          *(u32x2*)(vq + db * 32 + g4 * 8) = b;
+        }
+      }
+  }
+}
+
+// ---- launch
+
+template <int D>
+static hipError_t launch_bwd_d(const BwdParams& p, const Geometry& gq, const Geometry& gk, int32_t* plan_q,
+                               int32_t* plan_k, int64_t items_q, int64_t items_k, hipStream_t stream) {
+  const int64_t vectors = p.total_q * p.heads;
+  const int64_t per_block = 4 * (64 / (D / 8));
+  int64_t blocks = (vectors + per_block - 1) / per_block;
+  if (blocks > 8192) blocks = 8192;
+  if (blocks > 0) hipLaunchKernelGGL(bwd_stats_kernel<D>, dim3((unsigned)blocks), dim3(256), 0, stream, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  BwdParams pq = p;
+  pq.plan = plan_q;
+  pq.ng = gq.ng;
+  pq.n_hg = gq.n_hg;
+  if (items_q > 0)
+    hipLaunchKernelGGL(bwd_dq_kernel<D>, dim3((unsigned)(items_q * gq.n_hg)), dim3(64 * kBwdWaves), 0, stream, pq);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  BwdParams pk = p;
+  pk.plan = plan_k;
+  pk.ng = 1;
+  pk.n_hg = gk.n_hg;
+  const dim3 grid((unsigned)(items_k * gk.n_hg));
+  if (items_k > 0) {
+    if constexpr (D >= 256) {
+      hipLaunchKernelGGL((bwd_dkdv_kernel<D, 1>), grid, dim3(64 * kBwdWaves), 0, stream, pk);
+      hipLaunchKernelGGL((bwd_dkdv_kernel<D, 2>), grid, dim3(64 * kBwdWaves), 0, stream, pk);
+    } else {
+      hipLaunchKernelGGL((bwd_dkdv_kernel<D, 3>), grid, dim3(64 * kBwdWaves), 0, stream, pk);
+    }
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_bwd(const BwdParams& p, int head_dim, const Geometry& gq, const Geometry& gk, int32_t* plan_q,
+                      int32_t* plan_k, int64_t items_q, int64_t items_k, int tiles_q, int merges_q, int tiles_k,
+                      int merges_k, int32_t* tile_base, int n_seq, hipStream_t stream) {
+  // the two work lists: query tiles as the forward's, key tiles from the bounds swapped (a key j sees query rows
+  // i with j - right <= i + delta <= j + left: the window mirrored)
+  hipError_t e = launch_plan(p.q_cu, p.k_cu, n_seq, gq, p.left, p.right, plan_q, tiles_q, merges_q, (int)items_q,
+                             tile_base, stream);
+  if (e != hipSuccess) return e;
+  e = launch_plan(p.k_cu, p.q_cu, n_seq, gk, p.right, p.left, plan_k, tiles_k, merges_k, (int)items_k, tile_base,
+                  stream);
+  if (e != hipSuccess) return e;
+  switch (head_dim) {
+    case 64: return launch_bwd_d<64>(p, gq, gk, plan_q, plan_k, items_q, items_k, stream);
+    case 128: return launch_bwd_d<128>(p, gq, gk, plan_q, plan_k, items_q, items_k, stream);
+    case 256: return launch_bwd_d<256>(p, gq, gk, plan_q, plan_k, items_q, items_k, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace karpo

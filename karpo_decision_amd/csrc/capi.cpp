@@ -143,6 +143,8 @@ extern "C" int karpo_attn_fwd(const KarpoAttnArgs* a, void* stream) {
   if (a->gate != nullptr && (!aligned8(a->gate) || a->gate_stride_tok < 0 || a->gate_stride_head < 0 ||
                              a->gate_stride_tok % 4 != 0 || a->gate_stride_head % 4 != 0))
     return KARPO_ATTN_ERR_PROLOGUE;
+  if (a->lse != nullptr && (a->gate != nullptr || (reinterpret_cast<uintptr_t>(a->lse) & 3u) != 0))
+    return KARPO_ATTN_ERR_ARG;
 
   const Geometry g = geometry(a->heads, a->kv_heads, a->head_dim, a->max_q);
   // a step's key rows are addressed with 32-bit byte offsets
@@ -221,6 +223,8 @@ extern "C" int karpo_attn_fwd(const KarpoAttnArgs* a, void* stream) {
   p.gate = static_cast<const uint16_t*>(a->gate);
   p.sg_t = a->gate_stride_tok;
   p.sg_h = a->gate_stride_head;
+  p.lse = a->lse;
+  p.lse_stride = a->total_q;
   if (launch_forward(p, a->head_dim, g, z.items, merge ? z.merges : 0, s) != hipSuccess)
     return KARPO_ATTN_ERR_LAUNCH;
   return KARPO_ATTN_OK;
@@ -257,5 +261,133 @@ extern "C" int karpo_attn_norm_rope(const KarpoNormRopeArgs* a, void* stream) {
   p.rope_dim = a->rope_dim;
   p.eps = a->eps;
   if (launch_norm_rope(p, a->head_dim, static_cast<hipStream_t>(stream)) != hipSuccess) return KARPO_ATTN_ERR_LAUNCH;
+  return KARPO_ATTN_OK;
+}
+
+namespace {
+
+// The backward's workspace: per-row stats, then the query-tile and key-tile plans, then the planners' tile bases.
+struct BwdSizes {
+  int64_t tiles_q, tiles_k, stats_bytes, plan_q, plan_k, bytes;  // plan_q / plan_k: int offsets from the stats end
+};
+
+BwdSizes bwd_sizes_of(const KarpoAttnBwdArgs* b) {
+  const KarpoAttnArgs* a = &b->fwd;
+  const Geometry gq = bwd_geometry(a->heads, a->kv_heads, false);
+  BwdSizes z;
+  z.tiles_q = tile_capacity(a, gq);
+  z.tiles_k = (a->total_k + 32 * kBwdWaves - 1) / (32 * kBwdWaves) + a->n_seq;
+  z.stats_bytes = ((int64_t)a->heads * 2 * a->total_q * 4 + 255) / 256 * 256;
+  z.plan_q = 0;
+  z.plan_k = kPlanHeader + kItemInts * z.tiles_q;
+  const int64_t ints = z.plan_k + kPlanHeader + kItemInts * z.tiles_k + a->n_seq + 1;
+  z.bytes = z.stats_bytes + (ints * 4 + 255) / 256 * 256;
+  return z;
+}
+
+int check_bwd(const KarpoAttnBwdArgs* b) {
+  if (b == nullptr) return KARPO_ATTN_ERR_NULL;
+  const KarpoAttnArgs* a = &b->fwd;
+  const int st = check_shape(a);
+  if (st != KARPO_ATTN_OK) return st;
+  if (a->head_dim == 512) return KARPO_ATTN_ERR_HEAD_DIM;
+  if (a->total_k < 0) return KARPO_ATTN_ERR_ARG;
+  return KARPO_ATTN_OK;
+}
+
+}  // namespace
+
+extern "C" int karpo_attn_bwd_workspace_bytes(const KarpoAttnBwdArgs* b, size_t* bytes) {
+  const int st = check_bwd(b);
+  if (st != KARPO_ATTN_OK) return st;
+  if (bytes == nullptr) return KARPO_ATTN_ERR_NULL;
+  *bytes = (size_t)bwd_sizes_of(b).bytes;
+  return KARPO_ATTN_OK;
+}
+
+extern "C" int karpo_attn_bwd(const KarpoAttnBwdArgs* b, void* stream) {
+  int st = check_bwd(b);
+  if (st != KARPO_ATTN_OK) return st;
+  const KarpoAttnArgs* a = &b->fwd;
+  if (a->n_spans < 0 || (a->n_spans > 0 && a->spans == nullptr)) return KARPO_ATTN_ERR_SPANS;
+  if (a->plan != nullptr || a->k_rows != nullptr || a->q_norm != KARPO_NORM_NONE || a->rope_cos != nullptr ||
+      a->gate != nullptr)
+    return KARPO_ATTN_ERR_ARG;
+  if (a->total_q == 0 || a->n_seq == 0) return KARPO_ATTN_OK;
+  if (!a->q || !a->k || !a->v || !a->o || !a->q_cu || !a->k_cu || !b->d_o || !b->lse || !b->d_q || !b->d_k ||
+      !b->d_v)
+    return KARPO_ATTN_ERR_NULL;
+  if (a->total_k < 1) return KARPO_ATTN_ERR_ARG;
+  if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v) || !aligned16(a->o) || !aligned16(b->d_o) ||
+      !aligned16(b->d_q) || !aligned16(b->d_k) || !aligned16(b->d_v) ||
+      (reinterpret_cast<uintptr_t>(b->lse) & 3u) != 0)
+    return KARPO_ATTN_ERR_LAYOUT;
+  const int64_t strides[] = {a->q_stride_tok,    a->q_stride_head,    a->k_stride_tok,    a->k_stride_head,
+                             a->v_stride_tok,    a->v_stride_head,    a->o_stride_tok,    a->o_stride_head,
+                             b->d_o_stride_tok,  b->d_o_stride_head,  b->d_q_stride_tok,  b->d_q_stride_head,
+                             b->d_k_stride_tok,  b->d_k_stride_head,  b->d_v_stride_tok,  b->d_v_stride_head};
+  for (int64_t s : strides)
+    if (!check_stride(s)) return KARPO_ATTN_ERR_LAYOUT;
+  // a step's rows (32 keys, or 32 query rows) are addressed with 32-bit byte offsets
+  const int64_t d = a->head_dim;
+  if ((a->k_stride_tok + d) * kBwdStep * 2 >= (int64_t)INT32_MAX ||
+      (a->v_stride_tok + d) * kBwdStep * 2 >= (int64_t)INT32_MAX ||
+      (a->q_stride_tok + d) * kBwdStep * 2 >= (int64_t)INT32_MAX ||
+      (b->d_o_stride_tok + d) * kBwdStep * 2 >= (int64_t)INT32_MAX || (a->total_q + kBwdStep) * 4 >= INT32_MAX)
+    return KARPO_ATTN_ERR_LAYOUT;
+  const BwdSizes z = bwd_sizes_of(b);
+  const Geometry gq = bwd_geometry(a->heads, a->kv_heads, false);
+  const Geometry gk = bwd_geometry(a->heads, a->kv_heads, true);
+  if (z.tiles_q * gq.n_hg > (int64_t)INT32_MAX || z.tiles_k * gk.n_hg > (int64_t)INT32_MAX ||
+      z.plan_k + kPlanHeader + kItemInts * z.tiles_k > (int64_t)INT32_MAX)
+    return KARPO_ATTN_ERR_ARG;
+  if (a->workspace == nullptr || a->workspace_bytes < (size_t)z.bytes || !aligned16(a->workspace))
+    return KARPO_ATTN_ERR_WORKSPACE;
+
+  char* ws = static_cast<char*>(a->workspace);
+  int32_t* ints = reinterpret_cast<int32_t*>(ws + z.stats_bytes);
+  BwdParams p;
+  memset(&p, 0, sizeof(p));
+  p.q = static_cast<const uint16_t*>(a->q);
+  p.k = static_cast<const uint16_t*>(a->k);
+  p.v = static_cast<const uint16_t*>(a->v);
+  p.o = static_cast<const uint16_t*>(a->o);
+  p.dout = static_cast<const uint16_t*>(b->d_o);
+  p.lse = b->lse;
+  p.dq = static_cast<uint16_t*>(b->d_q);
+  p.dk = static_cast<uint16_t*>(b->d_k);
+  p.dv = static_cast<uint16_t*>(b->d_v);
+  p.stats = reinterpret_cast<float*>(ws);
+  p.sq_t = a->q_stride_tok;
+  p.sq_h = a->q_stride_head;
+  p.sk_t = a->k_stride_tok;
+  p.sk_h = a->k_stride_head;
+  p.sv_t = a->v_stride_tok;
+  p.sv_h = a->v_stride_head;
+  p.so_t = a->o_stride_tok;
+  p.so_h = a->o_stride_head;
+  p.sdo_t = b->d_o_stride_tok;
+  p.sdo_h = b->d_o_stride_head;
+  p.sdq_t = b->d_q_stride_tok;
+  p.sdq_h = b->d_q_stride_head;
+  p.sdk_t = b->d_k_stride_tok;
+  p.sdk_h = b->d_k_stride_head;
+  p.sdv_t = b->d_v_stride_tok;
+  p.sdv_h = b->d_v_stride_head;
+  p.q_cu = a->q_cu;
+  p.k_cu = a->k_cu;
+  p.spans = a->spans;
+  p.total_q = a->total_q;
+  p.n_spans = a->n_spans;
+  p.heads = a->heads;
+  p.group = a->heads / a->kv_heads;
+  p.left = a->window_left;
+  p.right = a->window_right;
+  p.c = a->scale * 1.4426950408889634f;
+  p.scale = a->scale;
+  if (launch_bwd(p, a->head_dim, gq, gk, ints + z.plan_q, ints + z.plan_k, z.tiles_q, z.tiles_k, (int)z.tiles_q, 0,
+                 (int)z.tiles_k, 0, ints + z.plan_k + kPlanHeader + kItemInts * z.tiles_k, a->n_seq,
+                 static_cast<hipStream_t>(stream)) != hipSuccess)
+    return KARPO_ATTN_ERR_LAUNCH;
   return KARPO_ATTN_OK;
 }

@@ -39,7 +39,37 @@ struct Params {
   int32_t q_norm;
   float q_eps;
   int32_t rope_dim;
+  float* __restrict__ lse;  // [heads][lse_stride] natural-log sums, or null
+  int64_t lse_stride;       // total_q
 };
+
+// The backward kernels' arguments (karpo_attn_bwd): the forward's tensors and bounds, the output gradient and the
+// gradients to write; stats holds (log2-domain LSE, rowsum(dO * O)) per (head, query row).
+struct BwdParams {
+  const uint16_t* __restrict__ q;
+  const uint16_t* __restrict__ k;
+  const uint16_t* __restrict__ v;
+  const uint16_t* __restrict__ o;
+  const uint16_t* __restrict__ dout;
+  const float* __restrict__ lse;
+  uint16_t* __restrict__ dq;
+  uint16_t* __restrict__ dk;
+  uint16_t* __restrict__ dv;
+  float* __restrict__ stats;  // [heads][2][total_q]: each row's log2-domain LSE, then rowsum(dout * o)
+  int64_t sq_t, sq_h, sk_t, sk_h, sv_t, sv_h, so_t, so_h, sdo_t, sdo_h, sdq_t, sdq_h, sdk_t, sdk_h, sdv_t, sdv_h;
+  const int32_t* __restrict__ q_cu;
+  const int32_t* __restrict__ k_cu;
+  const int32_t* __restrict__ spans;
+  const int32_t* __restrict__ plan;  // dq kernel: query tiles; dkdv kernel: key tiles
+  int64_t total_q;
+  int32_t n_spans, heads, group, ng, n_hg;
+  int32_t left, right;
+  float c;      // scale * log2(e) (signed)
+  float scale;  // the logit scale (signed): dq and dk carry it
+};
+hipError_t launch_bwd(const BwdParams& p, int head_dim, const Geometry& gq, const Geometry& gk, int32_t* plan_q,
+                      int32_t* plan_k, int64_t items_q, int64_t items_k, int tiles_q, int merges_q, int tiles_k,
+                      int merges_k, int32_t* tile_base, int n_seq, hipStream_t stream);
 
 // karpo_attn_norm_rope's kernel.
 struct NormRopeParams {

@@ -131,4 +131,24 @@ KA_HD inline int part_cost(int64_t steps, int parts) {
 KA_HD inline int64_t split_slots(const Geometry& g) { return 2 * (int64_t)g.conc / g.n_hg; }
 KA_HD inline int64_t split_tiles(const Geometry& g) { return split_slots(g) / 2; }
 
+// Backward tiles (attn_bwd.hip): four waves of 32 query vectors (dq kernel) or 32 keys (dkdv kernel), 32 keys or
+// query rows per step, never split (conc 1 makes the split length the whole pack).
+constexpr int kBwdWaves = 4;
+constexpr int kBwdStep = 32;
+// The dq kernel's query tiles (heads grouped as the forward groups them) and the dkdv kernel's key tiles (one
+// key/value head per item; the planner sees keys as queries and query rows as keys).
+KA_HD inline Geometry bwd_geometry(int heads, int kv_heads, bool key_tiles) {
+  Geometry g;
+  g.narrow = false;
+  g.waves = kBwdWaves;
+  g.vectors = 32 * kBwdWaves;
+  g.bn = kBwdStep;
+  const int group = heads / kv_heads;
+  g.ng = key_tiles ? 1 : (g.vectors % group == 0 ? group : 1);
+  g.rows = g.vectors / g.ng;
+  g.n_hg = key_tiles ? kv_heads : heads / g.ng;
+  g.conc = 1;
+  return g;
+}
+
 }  // namespace karpo

@@ -318,3 +318,112 @@ def norm_rope(x: Tensor, norm: Norm | None, rope: tuple[Tensor, Tensor] | None =
         _lib.check(lib.karpo_attn_norm_rope(ctypes.byref(a), ctypes.c_void_p(stream)), "norm_rope")
     # converted tables in `keep` go back to the stream-ordered caching allocator after the launch: safe to reuse
     return out
+
+
+# ---- training: the forward with its log-sum-exp and the backward, as a differentiable operator pair (the pattern of
+# karpo::fa4_sliding / karpo::fa4_sliding_backward, families/gemma/sliding_attention.py:36-66)
+
+def _workspace(lib, fn, args, device: torch.device) -> Tensor:
+    need = ctypes.c_size_t()
+    _lib.check(fn(ctypes.byref(args), ctypes.byref(need)), "packed attention")
+    return torch.empty(need.value, dtype=torch.uint8, device=device)
+
+
+@torch.library.custom_op(f"{NAMESPACE}::packed_attention_lse", mutates_args=())
+def packed_attention_lse(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_cu: Tensor, max_q: int,
+                         scale: float, window_left: int, window_right: int,
+                         spans: Tensor | None) -> tuple[Tensor, Tensor]:
+    """``packed_attention`` and its log-sum-exp: (Tq, heads, D) bf16 and (heads, Tq) fp32,
+    lse[h, i] = ln(sum over row i's visible keys of exp(scale * q.k)), -inf for a row that sees no key (the
+    reference's ``return_lse``, families/gemma/sliding_attention.py:39-41)."""
+    check_inputs(query, key, value, q_cu, k_cu)
+    if query.device.type != "cuda":
+        raise ValueError(f"packed attention runs on an MI355X GPU, not on {query.device}")
+    lib = _lib.load()
+    out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
+    lse = torch.empty((query.shape[1], query.shape[0]), dtype=torch.float32, device=query.device)
+    if query.shape[0] == 0:
+        return out, lse
+    q_cu, k_cu = q_cu.contiguous(), k_cu.contiguous()
+    with torch.cuda.device(query.device):
+        args = _args(query, key, value, out, q_cu, k_cu, q_cu.numel() - 1, max_q, scale, window_left, window_right,
+                     spans, None)
+        args.lse = lse.data_ptr()
+        workspace = _workspace(lib, lib.karpo_attn_workspace_bytes, args, query.device)
+        args.workspace, args.workspace_bytes = workspace.data_ptr(), workspace.numel()
+        stream = torch.cuda.current_stream(query.device).cuda_stream
+        _lib.check(lib.karpo_attn_fwd(ctypes.byref(args), ctypes.c_void_p(stream)), "packed attention")
+    return out, lse
+
+
+@packed_attention_lse.register_fake
+def _(query, key, value, q_cu, k_cu, max_q, scale, window_left, window_right, spans):
+    return query.new_empty(query.shape), query.new_empty((query.shape[1], query.shape[0]), dtype=torch.float32)
+
+
+@torch.library.custom_op(f"{NAMESPACE}::packed_attention_backward", mutates_args=())
+def packed_attention_backward(grad: Tensor, query: Tensor, key: Tensor, value: Tensor, out: Tensor, lse: Tensor,
+                              q_cu: Tensor, k_cu: Tensor, max_q: int, scale: float, window_left: int,
+                              window_right: int, spans: Tensor | None) -> tuple[Tensor, Tensor, Tensor]:
+    """Gradients of ``packed_attention_lse``'s output (dq, dk, dv, bf16, the shapes of query, key and value) from
+    the output gradient ``grad``, the forward's output and lse (``karpo_attn_bwd``). Rows outside the sequences'
+    bounds are not written."""
+    check_inputs(query, key, value, q_cu, k_cu)
+    for name, t in (("grad", grad), ("out", out)):
+        if t.shape != query.shape or t.dtype != torch.bfloat16 or t.device != query.device:
+            raise ValueError(f"{name} must be bf16 of the query's shape on its device")
+    if lse.shape != (query.shape[1], query.shape[0]) or lse.dtype != torch.float32 or not lse.is_contiguous():
+        raise ValueError("lse must be the forward's contiguous (heads, rows) fp32 tensor")
+    lib = _lib.load()
+    grad = grad if grad.stride(-1) == 1 and grad.stride(0) % 8 == 0 and grad.stride(1) % 8 == 0 else grad.contiguous()
+    dq = torch.empty(query.shape, dtype=query.dtype, device=query.device)
+    dk = torch.empty(key.shape, dtype=key.dtype, device=key.device)
+    dv = torch.empty(value.shape, dtype=value.dtype, device=value.device)
+    if query.shape[0] == 0:
+        return dq, dk.zero_(), dv.zero_()
+    q_cu, k_cu = q_cu.contiguous(), k_cu.contiguous()
+    with torch.cuda.device(query.device):
+        b = _lib.KarpoAttnBwdArgs()
+        b.fwd = _args(query, key, value, out, q_cu, k_cu, q_cu.numel() - 1, max_q, scale, window_left, window_right,
+                      spans, None)
+        b.fwd.total_k = key.shape[0]
+        b.d_o, b.d_o_stride_tok, b.d_o_stride_head = grad.data_ptr(), grad.stride(0), grad.stride(1)
+        b.lse = lse.data_ptr()
+        b.d_q, b.d_q_stride_tok, b.d_q_stride_head = dq.data_ptr(), dq.stride(0), dq.stride(1)
+        b.d_k, b.d_k_stride_tok, b.d_k_stride_head = dk.data_ptr(), dk.stride(0), dk.stride(1)
+        b.d_v, b.d_v_stride_tok, b.d_v_stride_head = dv.data_ptr(), dv.stride(0), dv.stride(1)
+        workspace = _workspace(lib, lib.karpo_attn_bwd_workspace_bytes, b, query.device)
+        b.fwd.workspace, b.fwd.workspace_bytes = workspace.data_ptr(), workspace.numel()
+        stream = torch.cuda.current_stream(query.device).cuda_stream
+        _lib.check(lib.karpo_attn_bwd(ctypes.byref(b), ctypes.c_void_p(stream)), "packed attention backward")
+    return dq, dk, dv
+
+
+@packed_attention_backward.register_fake
+def _(grad, query, key, value, out, lse, q_cu, k_cu, max_q, scale, window_left, window_right, spans):
+    return torch.empty_like(query), torch.empty_like(key), torch.empty_like(value)
+
+
+def _setup(ctx, inputs, output):
+    query, key, value, q_cu, k_cu, ctx.max_q, ctx.scale, ctx.window_left, ctx.window_right, spans = inputs
+    ctx.save_for_backward(query, key, value, *output, q_cu, k_cu, spans)
+
+
+def _gradient(ctx, grad, _lse_grad):
+    query, key, value, out, lse, q_cu, k_cu, spans = ctx.saved_tensors
+    dq, dk, dv = packed_attention_backward(grad.contiguous(), query, key, value, out, lse, q_cu, k_cu, ctx.max_q,
+                                           ctx.scale, ctx.window_left, ctx.window_right, spans)
+    return dq, dk, dv, None, None, None, None, None, None, None
+
+
+packed_attention_lse.register_autograd(_gradient, setup_context=_setup)
+
+
+def attention(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_cu: Tensor, max_q: int, scale: float,
+              window_left: int = -1, window_right: int = -1, spans: Tensor | None = None) -> Tensor:
+    """The differentiable packed attention (head sizes 64, 128 and 256): (Tq, heads, D) bf16; gradients flow to
+    query, key and value through ``karpo_attn_bwd``."""
+    if query.shape[2] not in (64, 128, 256):
+        raise ValueError(f"the backward takes head sizes 64, 128 and 256, not {query.shape[2]}")
+    return packed_attention_lse(query, key, value, q_cu, k_cu, int(max_q), float(scale), int(window_left),
+                                int(window_right), spans)[0]

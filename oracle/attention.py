@@ -104,3 +104,37 @@ def packed_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor
             o = torch.where(mask.any(-1)[None, None, :, None], o, torch.zeros((), dtype=o.dtype))
         out[dest] = o[0].transpose(0, 1)
     return out
+
+
+def packed_lse(query: torch.Tensor, key: torch.Tensor, q_cu: Sequence[int], k_cu: Sequence[int], scale: float,
+               window_left: int = -1, window_right: int = -1,
+               spans: Sequence[tuple[int, int]] = ()) -> torch.Tensor:
+    """(H, Tq) float64 log-sum-exp of each query row's scaled logits over its visible keys (the softmax normaliser
+    of ``packed_attention``; the reference's ``return_lse``, families/gemma/sliding_attention.py:39-41), -inf for a
+    row that sees no key."""
+    q_cu, k_cu = [int(x) for x in q_cu], [int(x) for x in k_cu]
+    group = query.shape[1] // key.shape[1]
+    q = query.to("cpu", torch.float64)
+    k = key.to("cpu", torch.float64).repeat_interleave(group, dim=1)
+    out = torch.full((query.shape[1], query.shape[0]), float("-inf"), dtype=torch.float64)
+    for qa, qb, ka, kb in zip(q_cu[:-1], q_cu[1:], k_cu[:-1], k_cu[1:]):
+        lq, lk = qb - qa, kb - ka
+        if lq == 0 or lk == 0:
+            continue
+        s = torch.einsum("qhd,khd->hqk", q[qa:qb], k[ka:kb]) * scale
+        q_id, k_id = span_ids(qa, lq, lk, spans)
+        mask = visible(lq, lk, window_left, window_right, q_id, k_id)
+        out[:, qa:qb] = torch.logsumexp(s.masked_fill(~mask[None], float("-inf")), dim=-1)
+    return out
+
+
+def packed_grads(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, grad: torch.Tensor,
+                 q_cu: Sequence[int], k_cu: Sequence[int], scale: float, window_left: int = -1,
+                 window_right: int = -1, spans: Sequence[tuple[int, int]] = (),
+                 dtype: torch.dtype = torch.float32) -> tuple[torch.Tensor, ...]:
+    """(out, dq, dk, dv) in ``dtype`` on the CPU: ``packed_attention`` and torch autograd's gradients of
+    sum(out * grad) (the backward the reference's attention ops compute, families/gemma/sliding_attention.py:50-61)."""
+    xs = [t.detach().to("cpu", dtype).requires_grad_(True) for t in (query, key, value)]
+    out = packed_attention(*xs, q_cu, k_cu, scale, window_left, window_right, spans, dtype=dtype)
+    out.backward(grad.to("cpu", dtype))
+    return (out.detach(), *(x.grad for x in xs))

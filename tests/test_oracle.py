@@ -205,3 +205,72 @@ def test_prologue_closed_forms():
     assert torch.equal(prologue.gate(o, torch.zeros_like(o)), o * 0.5)
     assert torch.allclose(prologue.gate(o, torch.full_like(o, 40.0)), o)
     assert torch.equal(prologue.gate(o, torch.full_like(o, -200.0)), torch.zeros_like(o) * o)
+
+
+# ---- the backward's oracle: log-sum-exp and gradients (oracle/attention.py packed_lse, packed_grads)
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+def test_lse_reweights_the_values_into_the_output(layout):
+    """exp(scale * q.k - lse) over the visible keys sums to 1 and averages v into the loop oracle's output; rows that
+    see no key have lse = -inf (the identity the backward's P = exp(s - lse) rests on)."""
+    q_lens, k_lens, left, right, local_spans = layout
+    q, k, v, q_cu, k_cu = _pack(q_lens, k_lens, 4, 2, 8, seed=11 + len(q_lens))
+    spans = [(q_cu[s] + a, q_cu[s] + b) for s, a, b in local_spans]
+    lse = oa.packed_lse(q, k, q_cu, k_cu, 0.7, left, right, spans)
+    want = brute.attention(q.numpy(), k.numpy(), v.numpy(), q_cu, k_cu, 0.7, left, right, spans)
+    for n in range(len(q_lens)):
+        qa, lq, ka, lk = q_cu[n], q_lens[n], k_cu[n], k_lens[n]
+        for i in range(lq):
+            row = qa + i
+            q_span = brute._span_of(row, spans)
+            for h in range(4):
+                seen = [j for j in range(lk) if brute.sees(i, j, lq, lk, left, right, q_span,
+                                                           brute._span_of(qa + j - (lk - lq), spans))]
+                if not seen:
+                    assert lse[h, row] == float("-inf")
+                    continue
+                w = np.array([math.exp(0.7 * float(q[row, h] @ k[ka + j, h // 2]) - float(lse[h, row]))
+                              for j in seen])
+                assert abs(w.sum() - 1.0) < 1e-12
+                np.testing.assert_allclose(w @ v[[ka + j for j in seen], h // 2].numpy(), want[row, h], atol=1e-12)
+
+
+def test_lse_of_zero_queries_counts_the_visible_keys():
+    q, k, _, q_cu, k_cu = _pack([20], [20], 2, 1, 4, seed=12)
+    lse = oa.packed_lse(torch.zeros_like(q), k, q_cu, k_cu, 1.0, 5, 0)
+    want = torch.log(torch.minimum(torch.arange(1, 21), torch.tensor(6)).double())
+    torch.testing.assert_close(lse, want[None].expand(2, 20), atol=1e-15, rtol=0)
+
+
+def test_gradients_are_the_oracles_derivative():
+    """torch autograd through the oracle against central differences (float64), with a window, a span, GQA and a
+    branch (Lk > Lq)."""
+    q, k, v, q_cu, k_cu = _pack([6, 5], [6, 8], 4, 2, 4, seed=13)
+    spans = [(1, 4)]
+
+    def f(q_, k_, v_):
+        return oa.packed_attention(q_, k_, v_, q_cu, k_cu, 0.6, 3, 0, spans, dtype=torch.float64)
+
+    xs = [t.clone().requires_grad_(True) for t in (q, k, v)]
+    assert torch.autograd.gradcheck(f, xs, eps=1e-6, atol=1e-8, rtol=1e-6)
+
+
+def test_value_gradient_of_zero_queries_is_a_causal_mean():
+    """q = 0, causal: out_i = mean(v_0..v_i), so dv_j = sum over i >= j of grad_i / (i + 1); dk = scale dS^T q = 0;
+    dq_i = scale * sum over j <= i of (dP_ij - rowsum(grad_i * out_i)) k_j / (i + 1) (a dS that drops the rowsum term
+    or a transposed dP fails it)."""
+    q, k, v, q_cu, k_cu = _pack([10], [10], 2, 1, 4, seed=14)
+    g = torch.randn(10, 2, 4, generator=torch.Generator().manual_seed(15), dtype=torch.float64)
+    out, dq, dk, dv = oa.packed_grads(torch.zeros_like(q), k, v, g, q_cu, k_cu, 1.0, -1, 0, dtype=torch.float64)
+    weights = 1.0 / torch.arange(1, 11, dtype=torch.float64)
+    want = torch.flip(torch.cumsum(torch.flip(g.sum(1) * weights[:, None], [0]), 0), [0])
+    torch.testing.assert_close(dv[:, 0], want, atol=1e-12, rtol=0)
+    # with q = 0, dk = scale * dS^T q = 0 exactly, whatever dS is
+    torch.testing.assert_close(dk, torch.zeros_like(dk), atol=1e-15, rtol=0)
+    # dq_i = scale * sum_j P_ij (dP_ij - D_i) k_j with P uniform over j <= i
+    for i in range(10):
+        for h in range(2):
+            p = torch.full((i + 1,), 1.0 / (i + 1), dtype=torch.float64)
+            dp = v[: i + 1, 0] @ g[i, h]
+            d = (g[i, h] * out[i, h]).sum()
+            torch.testing.assert_close(dq[i, h], (p * (dp - d)) @ k[: i + 1, 0], atol=1e-12, rtol=0)
