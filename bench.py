@@ -46,6 +46,10 @@ def parse() -> argparse.Namespace:
     p.add_argument("--materialize-gather", action="store_true",
                    help="for workloads with a gather table: time index_select copies of K/V plus the attention on "
                         "them (the reference's Packed._gather path) instead of reading through the table")
+    p.add_argument("--backward", action="store_true",
+                   help="time the backward (karpo_attn_bwd: dq, dk, dv from the output gradient, the forward's "
+                        "output and log-sum-exp) instead of the forward; head sizes 64, 128 and 256, no gather or "
+                        "fused prologue")
     p.add_argument("--copy-bytes", type=int, default=0,
                    help="after the timed steps, copy this many bytes device to device once (a calibration kernel of "
                         "known traffic for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -149,6 +153,101 @@ def keys_norm_rope(args, device) -> int:
     return 0
 
 
+def copy_once(nbytes: int, device) -> None:
+    """One device-to-device copy of ``nbytes`` (a kernel of known traffic to calibrate FETCH_SIZE / WRITE_SIZE)."""
+    import torch
+
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device=device)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+
+
+def cpu_backward_baseline(w) -> dict:
+    """The oracle's gradients (torch autograd through the per-sequence CPU SDPA path) on one KV-head group of the
+    pack, float32, one run (the backward at 32k tokens takes seconds per group)."""
+    import torch
+
+    from oracle import attention as oracle_attention
+
+    torch.set_num_threads(int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)))
+    group = w.heads // w.kv_heads
+    q, k, v = w.query[:, :group].cpu(), w.key[:, :1].cpu(), w.value[:, :1].cpu()
+    grad = torch.randn(q.shape, generator=torch.Generator().manual_seed(1)).to(q.dtype)
+    t0 = time.perf_counter()
+    oracle_attention.packed_grads(q, k, v, grad, w.q_cu, w.k_cu, w.scale, w.window_left, w.window_right, w.spans,
+                                  dtype=torch.float32)
+    sec = time.perf_counter() - t0
+    sample_flops = 2.5 * w.flops() * group / w.heads
+    return {"value": round(sample_flops / sec / 1e12, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": (f"{w.name} backward: query heads 0-{group - 1} (KV head 0) of {w.heads}, all {w.tokens} "
+                       f"tokens; torch {torch.__version__} CPU SDPA per sequence + autograd, float32, one run "
+                       f"{sec:.3f} s; os.cpu_count()={os.cpu_count()}")}
+
+
+def backward(args, device, w) -> int:
+    """One step = karpo_attn_bwd over the pack (the statistics pass, the dq kernel, the dk/dv kernel and their two
+    planner launches) from a resident output gradient, output and log-sum-exp. TFLOP/s counts the algorithmic
+    backward: 2.5x the forward's FLOPs (five products per visible pair: S, dP, dV, dQ, dK)."""
+    import torch
+
+    from karpo_decision_amd import ops
+
+    if w.key_rows is not None or w.q_norm is not None or w.rope is not None or w.gate is not None:
+        raise SystemExit(f"--backward takes workloads without gather tables or fused prologues, not {w.name}")
+    q_cu = torch.tensor(w.q_cu, dtype=torch.int32, device=device)
+    k_cu = torch.tensor(w.k_cu, dtype=torch.int32, device=device)
+    spans = torch.tensor(w.spans, dtype=torch.int32, device=device) if w.spans else None
+    out, lse = ops.packed_attention_lse(w.query, w.key, w.value, q_cu, k_cu, w.max_q, w.scale, w.window_left,
+                                        w.window_right, spans)
+    gen = torch.Generator(device=device).manual_seed(args.seed + 1)
+    grad = torch.randn(out.shape, generator=gen, device=device).to(out.dtype)
+
+    def step():
+        return ops.packed_attention_backward(grad, w.query, w.key, w.value, out, lse, q_cu, k_cu, w.max_q, w.scale,
+                                             w.window_left, w.window_right, spans)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(device)
+    marks = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    begin.record(stream)
+    for a, b in marks:
+        a.record(stream)
+        step()
+        b.record(stream)
+    end.record(stream)
+    torch.cuda.synchronize()
+    if args.copy_bytes:
+        copy_once(args.copy_bytes, device)
+    ms_per_step = begin.elapsed_time(end) / args.steps
+    launch_ms = statistics.mean(a.elapsed_time(b) for a, b in marks)
+    flops = 2.5 * w.flops()
+    value = flops / (ms_per_step * 1e-3) / 1e12
+    achieved = flops / (launch_ms * 1e-3) / 1e12
+    result = {
+        "metric": "packed causal attention backward TFLOP/s + % bf16 MFMA peak, 1 GPU", "value": round(value, 2),
+        "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {**w.describe(), "pass": "backward", "pct_of_bf16_peak": round(100 * value / PEAK_BF16_TFLOPS, 2),
+                   "flops_per_step": flops, "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "kernel": f"karpo_attn_bwd (bwd_stats_kernel, bwd_dq_kernel<{w.head_dim}>, "
+                               f"bwd_dkdv_kernel<{w.head_dim}, *>)",
+                     "avg_launch_ms": round(launch_ms, 4)},
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_backward_baseline(w)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -163,6 +262,8 @@ def main() -> int:
     if args.workload == "keys_norm_rope":
         return keys_norm_rope(args, device)
     w = workloads.named(args.workload, device, args.seed)
+    if args.backward:
+        return backward(args, device, w)
     q_cu = torch.tensor(w.q_cu, dtype=torch.int32, device=device)
     k_cu = torch.tensor(w.k_cu, dtype=torch.int32, device=device)
     spans = torch.tensor(w.spans, dtype=torch.int32, device=device) if w.spans else None
@@ -202,12 +303,7 @@ def main() -> int:
         end.record(stream)
         torch.cuda.synchronize()
     if args.copy_bytes:
-        src = torch.ones(args.copy_bytes // 4, dtype=torch.float32, device=device)
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
+        copy_once(args.copy_bytes, device)
     total_ms = begin.elapsed_time(end)
     launch_ms = statistics.mean(a.elapsed_time(b) for a, b in marks)
     ms_per_step = total_ms / args.steps

@@ -15,7 +15,13 @@
 //   * bwd_dkdv_kernel (key-stationary, tiles of 128 keys, four waves of 32): K and V of the wave's keys in registers,
 //     the query rows that see the tile streamed in steps of 32 rows of one head (every head of the GQA group in turn,
 //     which sums the group's gradients): S = Q K^T and dP = dO V^T with Q and dO as row operands, dV^T += dO^T P and
-//     dK^T += Q^T dS with Q and dO read transposed, so Q and dO are staged in both layouts.
+//     dK^T += Q^T dS with Q and dO read transposed, so Q and dO are staged in both layouts. One launch computes both
+//     (MODE 3), or two launches compute dV (MODE 1) and dK (MODE 2), each recomputing S: always at head size 256
+//     (both accumulators and both operands do not fit one wave's registers), and at 128 for packs with many key tiles
+//     (two or three waves per SIMD instead of one overlap each other's softmax and MFMA work; a small pack has too
+//     few tiles to fill the GPU twice).
+// Both streams advance their copy addresses by pointer increments per step (no per-step address recomputation: the
+// scalar unit is shared by the CU's waves and a step is short).
 // Rows of a product's row operand are fed in the order that swaps bits 2 and 3 of the row index (key_row), so each
 // lane's 8 consecutive result registers are 8 consecutive rows: P, dS (S^T layout) are directly the B operands of the
 // next products, as in the forward.
@@ -32,9 +38,12 @@ namespace karpo {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// Key-tile workgroups from which head size 128 runs dK and dV as two launches.
+constexpr int64_t kSplitKeyTiles = 8 * kComputeUnits;
+
 template <int D> struct BwdCfg {
   static constexpr int OCC_Q = D >= 256 ? 1 : 2;  // waves per SIMD the registers are budgeted for
-  static constexpr int OCC_K = 1;
+  template <int MODE> static constexpr int occ_k() { return MODE == 3 || D >= 256 ? 1 : MODE == 1 ? 3 : 2; }
 };
 
 // Row (within a 32-row step) of result register j of a lane in half `half` (row operands fed in key_row order).
@@ -193,10 +202,15 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::OCC_Q) void bwd_dq_kerne
     v_dma_source<D>(wave * INSTS + r, lane, &key, &colm);
     kv_off[r] = (uint32_t)(key * p.sk_t + colm) * 2u;
   }
+  const uint16_t* c_k = kbase + (int64_t)j_first * p.sk_t;
+  const uint16_t* c_v = vbase + (int64_t)j_first * p.sv_t;
+  const int64_t k_step = (int64_t)BN * p.sk_t, v_step = (int64_t)BN * p.sv_t;
   auto copy_step = [&](int j0, KA_LDS char* tkk, KA_LDS char* tkv, KA_LDS char* tvk) {
     const int rows = min(lk - j0, BN);
-    const uint16_t* ks = kbase + (int64_t)j0 * p.sk_t;
-    const uint16_t* vs = vbase + (int64_t)j0 * p.sv_t;
+    const uint16_t* ks = c_k;
+    const uint16_t* vs = c_v;
+    c_k += k_step;
+    c_v += v_step;
 #pragma unroll
     for (int r = 0; r < INSTS; ++r)
       if (BLKS % W == 0 || wave * INSTS + r < BLKS) {
@@ -291,10 +305,9 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::OCC_Q) void bwd_dq_kerne
 }
 
 // ---- dK, dV: key tiles of 128 (plan items of the bounds swapped: segment, key tile), 32 keys per wave. MODE bit 0:
-// compute dV, bit 1: dK (head size 256 runs the two as separate launches: both accumulators and both operands do not
-// fit one wave's registers).
+// compute dV, bit 1: dK.
 template <int D, int MODE>
-__global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::OCC_K) void bwd_dkdv_kernel(BwdParams p) {
+__global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::template occ_k<MODE>()) void bwd_dkdv_kernel(BwdParams p) {
   constexpr bool DV = (MODE & 1) != 0, DK = (MODE & 2) != 0;
   constexpr int W = kBwdWaves, BQ = kBwdStep;
   constexpr int DC = D / 16, DB = D / 32, KC = BQ / 16;
@@ -411,13 +424,31 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::OCC_K) void bwd_dkdv_ker
     ov_off[r] = (uint32_t)(row * p.sdo_t + colm) * 2u;
   }
   // step s: head kvh * group + s / n_rsteps, rows r_first + (s % n_rsteps) * BQ ..
+  const int r_end = r_first + n_rsteps * BQ;
+  const int h0 = kvh * p.group;
+  const int64_t q_step = (int64_t)BQ * p.sq_t, o_step = (int64_t)BQ * p.sdo_t;
+  const int64_t q_wrap = p.sq_h - n_rsteps * q_step, o_wrap = p.sdo_h - n_rsteps * o_step;
+  const int64_t st_wrap = 2 * p.total_q - (int64_t)n_rsteps * BQ;
+  int c_r0 = r_first;
+  const uint16_t* c_q = p.q + (int64_t)(qa + r_first) * p.sq_t + (int64_t)h0 * p.sq_h;
+  const uint16_t* c_o = p.dout + (int64_t)(qa + r_first) * p.sdo_t + (int64_t)h0 * p.sdo_h;
+  const float* c_st = p.stats + (int64_t)h0 * 2 * p.total_q + qa + r_first;
   auto copy_step = [&](int s, KA_LDS char* tqk, KA_LDS char* tqv, KA_LDS char* tok, KA_LDS char* tov,
                        KA_LDS float* tst) {
-    const int h = kvh * p.group + s / n_rsteps;
-    const int r0 = r_first + (s % n_rsteps) * BQ;
-    const int rows = min(lq - r0, BQ);
-    const uint16_t* qs = p.q + (int64_t)(qa + r0) * p.sq_t + (int64_t)h * p.sq_h;
-    const uint16_t* os = p.dout + (int64_t)(qa + r0) * p.sdo_t + (int64_t)h * p.sdo_h;
+    const int rows = min(lq - c_r0, BQ);
+    const uint16_t* qs = c_q;
+    const uint16_t* os = c_o;
+    const float* src = c_st;
+    c_r0 += BQ;
+    c_q += q_step;
+    c_o += o_step;
+    c_st += BQ;
+    if (c_r0 == r_end) {
+      c_r0 = r_first;
+      c_q += q_wrap;
+      c_o += o_wrap;
+      c_st += st_wrap;
+    }
 #pragma unroll
     for (int r = 0; r < INSTS; ++r)
       if (BLKS % W == 0 || wave * INSTS + r < BLKS) {
@@ -430,7 +461,6 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::OCC_K) void bwd_dkdv_ker
         if constexpr (DV) dma_16b(os, rows * (int)p.sdo_t * 2, tov + at, ov_off[r]);
       }
     if (wave == W - 1) {  // 32 log2 LSE (lanes 0-31) then 32 D (lanes 32-63), 4 B per lane; zeros past the stats
-      const float* src = p.stats + (int64_t)h * 2 * p.total_q + qa + r0;
       const __amdgpu_buffer_rsrc_t rs =
           __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, (int)(p.total_q + rows) * 4, kBufferFlags);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (KA_LDS void*)tst, 4,
@@ -458,6 +488,7 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::OCC_K) void bwd_dkdv_ker
   KA_LDS char* const tov1 = (KA_LDS char*)ov1;
   KA_LDS float* const tst0 = (KA_LDS float*)sts0;
   KA_LDS float* const tst1 = (KA_LDS float*)sts1;
+  int r_cur = r_first;
   if (n_steps > 0) copy_step(0, tqk0, tqv0, tok0, tov0, tst0);
   wait_vmcnt<0>();
   __syncthreads();
@@ -466,7 +497,8 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::OCC_K) void bwd_dkdv_ker
                   const KA_LDS char* tov, const KA_LDS float* tst, KA_LDS char* nqk, KA_LDS char* nqv,
                   KA_LDS char* nok, KA_LDS char* nov, KA_LDS float* nst) {
     if (s + 1 < n_steps) copy_step(s + 1, nqk, nqv, nok, nov, nst);
-    const int r0 = r_first + (s % n_rsteps) * BQ;
+    const int r0 = r_cur;
+    r_cur = r_cur + BQ == r_end ? r_first : r_cur + BQ;
     if (r0 < whi && r0 + BQ > wlo) {
       f32x16 st = f32x16{}, dpt = f32x16{};
 #pragma unroll
@@ -585,10 +617,12 @@ static hipError_t launch_bwd_d(const BwdParams& p, const Geometry& gq, const Geo
   pk.n_hg = gk.n_hg;
   const dim3 grid((unsigned)(items_k * gk.n_hg));
   if (items_k > 0) {
-    if constexpr (D >= 256) {
-      hipLaunchKernelGGL((bwd_dkdv_kernel<D, 1>), grid, dim3(64 * kBwdWaves), 0, stream, pk);
-      hipLaunchKernelGGL((bwd_dkdv_kernel<D, 2>), grid, dim3(64 * kBwdWaves), 0, stream, pk);
-    } else {
+    if (D >= 256 || (D == 128 && items_k * gk.n_hg >= kSplitKeyTiles)) {
+      if constexpr (D >= 128) {
+        hipLaunchKernelGGL((bwd_dkdv_kernel<D, 1>), grid, dim3(64 * kBwdWaves), 0, stream, pk);
+        hipLaunchKernelGGL((bwd_dkdv_kernel<D, 2>), grid, dim3(64 * kBwdWaves), 0, stream, pk);
+      }
+    } else if constexpr (D <= 128) {
       hipLaunchKernelGGL((bwd_dkdv_kernel<D, 3>), grid, dim3(64 * kBwdWaves), 0, stream, pk);
     }
   }

@@ -136,3 +136,15 @@ def test_backward_refuses_what_it_does_not_take(gpu):
     out, lse = ops.packed_attention_lse(q, q, q, cu, cu, 8, 0.1, -1, 0, None)
     with pytest.raises(ValueError):
         ops.packed_attention_backward(out, q, q, q, out, lse[:, :4], cu, cu, 8, 0.1, -1, 0, None)
+
+
+def test_many_key_tiles_take_the_two_launch_path(gpu):
+    """Head size 128 with 32 key/value heads over 8,192 keys: enough key tiles for dK and dV to run as two launches
+    (each recomputing P), against the oracle like the one-launch packs above."""
+    q, k, v, do, q_cu, k_cu, spans = make_pack([6000, 2192], [6000, 2192], 32, 32, 128, seed=31)
+    got = kernel_grads(q, k, v, do, q_cu, k_cu, 128 ** -0.5, -1, 0, spans)
+    want = oa.packed_grads(q, k, v, do, q_cu, k_cu, 128 ** -0.5, -1, 0, spans, dtype=torch.float32)
+    for name, x, w in zip(("out", "dq", "dk", "dv"), got, want):
+        r = rel(x, w)
+        print(name, f"rel {r:.2e}", flush=True)
+        assert r < REL_FRO, (name, r)
