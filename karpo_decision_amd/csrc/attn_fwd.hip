@@ -390,9 +390,14 @@ __global__ __launch_bounds__((64 * TileCfg<D, NARROW>::W), (TileCfg<D, NARROW>::
   auto gathered = [&](int row, uint32_t colb, int64_t stride) -> uint32_t {
     return (unsigned)row < (unsigned)p.total_k ? (uint32_t)row * (uint32_t)(stride * 2) + colb : 0xffffffffu;
   };
+  // copies run in step order: the step's first key row pointers advance by increments (no per-step multiply)
+  const uint16_t* c_k = kbase + (GATHER ? 0 : (int64_t)j_first * p.sk_t);
+  const uint16_t* c_v = vbase + (GATHER ? 0 : (int64_t)j_first * p.sv_t);
+  const int64_t k_step = GATHER ? 0 : (int64_t)BN * p.sk_t, v_step = GATHER ? 0 : (int64_t)BN * p.sv_t;
   auto copy_k = [&](int j0, KA_LDS char* kt) {
     const int rows = min(lk - j0, BN);
-    const uint16_t* ks = kbase + (GATHER ? 0 : (int64_t)j0 * p.sk_t);
+    const uint16_t* ks = c_k;
+    c_k += k_step;
 #pragma unroll
     for (int r = 0; r < INSTS; ++r)
       if (BLKS % W == 0 || wave * INSTS + r < BLKS) {
@@ -404,7 +409,8 @@ __global__ __launch_bounds__((64 * TileCfg<D, NARROW>::W), (TileCfg<D, NARROW>::
   };
   auto copy_v = [&](int j0, KA_LDS char* vt) {
     const int rows = min(lk - j0, BN);
-    const uint16_t* vs = vbase + (GATHER ? 0 : (int64_t)j0 * p.sv_t);
+    const uint16_t* vs = c_v;
+    c_v += v_step;
 #pragma unroll
     for (int r = 0; r < INSTS; ++r)
       if (BLKS % W == 0 || wave * INSTS + r < BLKS) {

@@ -212,6 +212,8 @@ class Plan:
     items: int
     rows_per_tile: int
     split_tiles: int
+    query_end: int = 0  # q_cu[-1] and k_cu[-1]: the rows the bounds index (checked against the tensors in ``run``)
+    key_end: int = 0
 
     @property
     def header(self) -> list[int]:
@@ -247,7 +249,7 @@ def make_plan(q_cu: list[int] | Tensor, k_cu: list[int] | Tensor, heads: int, kv
     used = buf[6] + 4 * buf[0]
     host = torch.tensor(list(buf[:used]), dtype=torch.int32)
     return Plan(host.to(device), heads, kv_heads, head_dim, window_left, window_right, max_q, int(buf[0]),
-                int(buf[1]), int(buf[4]))
+                int(buf[1]), int(buf[4]), qc[-1], kc[-1])
 
 
 def key_rows_of(rows: Tensor | None) -> Tensor | None:
@@ -272,6 +274,13 @@ def run(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_cu: Tensor, m
         if _lib.tile_shape(plan.heads, plan.kv_heads, plan.head_dim, plan.max_q) != _lib.tile_shape(
                 plan.heads, plan.kv_heads, plan.head_dim, int(max_q)):
             raise ValueError(f"the plan was made for max_q {plan.max_q}, another tile shape than max_q {max_q}")
+        # the plan's host bounds: rows past the tensors would be read out of their allocations
+        if plan.query_end > query.shape[0]:
+            raise ValueError(f"the bounds index {plan.query_end} query rows, the query has {query.shape[0]}")
+        key_rows_len = key.shape[0] if key_rows is None else key_rows.shape[0]
+        if plan.key_end > key_rows_len:
+            raise ValueError(f"the bounds index {plan.key_end} key rows, the {'key' if key_rows is None else 'row table'}"
+                             f" has {key_rows_len}")
         tensor, split_tiles = plan.tensor, plan.split_tiles
     mode, eps, weight = NORM_NONE, 0.0, None
     if q_norm is not None:

@@ -8,6 +8,7 @@ import re
 from pathlib import Path
 
 import pytest
+import torch
 from hypothesis import given, settings
 from hypothesis import strategies as st
 
@@ -233,6 +234,22 @@ def test_python_plan_object():
     assert long.split_tiles == 8 and long.items == 16 + 8
     with pytest.raises(ValueError):
         ops.make_plan([0, 100, 400], [0, 100, 400], 32, 16, 128, -1, 0, device="cpu", max_q=10)
+
+
+def test_planned_call_refuses_bounds_past_the_tensors():
+    """A plan knows its host bounds: a call whose bounds index rows past the query, the keys or the row table is
+    refused before anything runs (the kernel would read past the allocations)."""
+    plan = ops.make_plan([0, 100, 400], [0, 300, 900], 4, 2, 64, -1, 0, device="cpu")
+    assert (plan.query_end, plan.key_end) == (400, 900)
+    q = torch.zeros(400, 4, 64, dtype=torch.bfloat16)
+    k = torch.zeros(500, 2, 64, dtype=torch.bfloat16)
+    cu = torch.zeros(3, dtype=torch.int32)
+    with pytest.raises(ValueError, match="900 key rows"):
+        ops.run(q, k, k, cu, cu, 300, 0.1, -1, 0, None, plan)
+    with pytest.raises(ValueError, match="row table"):
+        ops.run(q, k, k, cu, cu, 300, 0.1, -1, 0, None, plan, key_rows=torch.zeros(800, dtype=torch.int32))
+    with pytest.raises(ValueError, match="query rows"):
+        ops.run(q[:399], k, k, cu, cu, 300, 0.1, -1, 0, None, plan, key_rows=torch.zeros(900, dtype=torch.int32))
 
 
 @pytest.mark.parametrize("q_cu,k_cu,left,right,spans", [
