@@ -43,6 +43,7 @@ constexpr int64_t kSplitKeyTiles = 8 * kComputeUnits;
 
 template <int D> struct BwdCfg {
   static constexpr int OCC_Q = D >= 256 ? 1 : 2;  // waves per SIMD the registers are budgeted for
+  static constexpr int BLOCKS_Q = OCC_Q * 4 / bwd_q_waves(D) > 0 ? OCC_Q * 4 / bwd_q_waves(D) : 1;
   template <int MODE> static constexpr int occ_k() { return MODE == 3 || D >= 256 ? 1 : MODE == 1 ? 3 : 2; }
 };
 
@@ -79,10 +80,10 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(BwdParams p) {
   }
 }
 
-// ---- dQ: the forward's query tiles (plan items: segment, tile), 32 query vectors per wave
+// ---- dQ: query tiles (plan items: segment, tile), 32 query vectors per wave, BN keys (KB blocks of 32) per step
 template <int D>
-__global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::OCC_Q) void bwd_dq_kernel(BwdParams p) {
-  constexpr int W = kBwdWaves, BN = kBwdStep;
+__global__ __launch_bounds__(64 * bwd_q_waves(D), BwdCfg<D>::BLOCKS_Q) void bwd_dq_kernel(BwdParams p) {
+  constexpr int W = bwd_q_waves(D), BN = bwd_q_step(D), KB = BN / 32;
   constexpr int DC = D / 16, DB = D / 32, KC = BN / 16;
   constexpr int TILE = BN * D * 2, BLKS = TILE / 1024, INSTS = (BLKS + W - 1) / W;
   __shared__ __attribute__((aligned(1024))) char kk0[TILE];  // K, row-operand layout
@@ -243,28 +244,47 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::OCC_Q) void bwd_dq_kerne
     const int j0 = j_first + s * BN;
     if (s + 1 < n_steps) copy_step(j0 + BN, nkk, nkv, nvk);
     if (j0 < whi && j0 + BN > wlo) {
-      f32x16 st = f32x16{}, dpt = f32x16{};
+      f32x16 st[KB], dpt[KB];
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        st[kb] = f32x16{};
+        dpt[kb] = f32x16{};
+      }
 #pragma unroll
       for (int dc = 0; dc < DC; ++dc) {
-        const bf16x8 a = *(const KA_LDS bf16x8*)(tkk + k_read + dc * 512);
-        st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qop[dc], st, 0, 0, 0);
-        const bf16x8 b = *(const KA_LDS bf16x8*)(tvk + k_read + dc * 512);
-        dpt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, dop[dc], dpt, 0, 0, 0);
-      }
-      const bool partial = !(j0 >= wflo && j0 + BN <= wfhi);
-      bf16x8 dsb[KC];
 #pragma unroll
-      for (int kc = 0; kc < KC; ++kc) {
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-          const int jj = kc * 8 + t;
-          const int key = j0 + (jj >> 3) * 16 + half * 8 + (jj & 7);
-          const bool vis = !partial || (((unsigned)(key - lo) < (unsigned)(hi - lo)) |
-                                        ((unsigned)(key - sl) < (unsigned)(sh - sl)));
-          const float pr = vis ? __builtin_amdgcn_exp2f(__builtin_fmaf(st[jj], c, -lse2)) : 0.f;
-          dsb[kc][t] = (__bf16)(pr * (dpt[jj] - dsum));
+        for (int kb = 0; kb < KB; ++kb) {  // key block kb: rows kb * 32 .. of the step
+          const int at = k_read + kb * (2 * (D / 8) * 256) + dc * 512;
+          const bf16x8 a = *(const KA_LDS bf16x8*)(tkk + at);
+          st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qop[dc], st[kb], 0, 0, 0);
+          const bf16x8 b = *(const KA_LDS bf16x8*)(tvk + at);
+          dpt[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, dop[dc], dpt[kb], 0, 0, 0);
         }
       }
+      // exponents of P^T (key kc * 16 + half * 8 + t of the step: register (kc & 1) * 8 + t of key block kc / 2);
+      // on a step some lane's window or span cuts, -inf (exp2 gives 0) for the keys that lane does not see: one
+      // uniform branch around the masking, none per element and no mask work on the other steps
+      float x[KC][8];
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) x[kc][t] = __builtin_fmaf(st[kc >> 1][(kc & 1) * 8 + t], c, -lse2);
+      if (!(j0 >= wflo && j0 + BN <= wfhi)) {
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+          for (int t = 0; t < 8; ++t) {
+            const int key = j0 + kc * 16 + half * 8 + t;
+            const bool vis = ((unsigned)(key - lo) < (unsigned)(hi - lo)) | ((unsigned)(key - sl) < (unsigned)(sh - sl));
+            x[kc][t] = vis ? x[kc][t] : -INFINITY;
+          }
+      }
+      bf16x8 dsb[KC];
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+          dsb[kc][t] = (__bf16)(__builtin_amdgcn_exp2f(x[kc][t]) * (dpt[kc >> 1][(kc & 1) * 8 + t] - dsum));
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc) {
 #pragma unroll
@@ -518,22 +538,30 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::template occ_k<MODE>()) 
         ls[u] = *(const KA_LDS f32x4*)(tst + r);
         ds[u] = *(const KA_LDS f32x4*)(tst + BQ + r);
       }
-      const bool partial = !(r0 >= wflo && r0 + BQ <= wfhi);
+      // exponents of P; on a step some lane's window or span cuts, -inf for the rows that do not see the lane's key
+      // (one uniform branch around the masking)
+      float x[2 * KC * 4];
+#pragma unroll
+      for (int jj = 0; jj < 2 * KC * 4; ++jj) x[jj] = __builtin_fmaf(st[jj], c, -ls[jj >> 2][jj & 3]);
+      if (!(r0 >= wflo && r0 + BQ <= wfhi)) {
+#pragma unroll
+        for (int jj = 0; jj < 2 * KC * 4; ++jj) {
+          const int row = r0 + result_row(jj, half);
+          const bool vis =
+              ((unsigned)(row - rlo) < (unsigned)(rhi - rlo)) | ((unsigned)(row - srl) < (unsigned)(srh - srl));
+          x[jj] = vis ? x[jj] : -INFINITY;
+        }
+      }
       bf16x8 pb[KC], dsb[KC];
 #pragma unroll
-      for (int kc = 0; kc < KC; ++kc) {
+      for (int kc = 0; kc < KC; ++kc)
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
           const int jj = kc * 8 + t;
-          const int row = r0 + result_row(jj, half);
-          const bool vis = !partial || (((unsigned)(row - rlo) < (unsigned)(rhi - rlo)) |
-                                        ((unsigned)(row - srl) < (unsigned)(srh - srl)));
-          const float l2 = ls[jj >> 2][jj & 3], dd = ds[jj >> 2][jj & 3];
-          const float pr = vis ? __builtin_amdgcn_exp2f(__builtin_fmaf(st[jj], c, -l2)) : 0.f;
+          const float pr = __builtin_amdgcn_exp2f(x[jj]);
           if constexpr (DV) pb[kc][t] = (__bf16)pr;
-          if constexpr (DK) dsb[kc][t] = (__bf16)(pr * (dpt[jj] - dd));
+          if constexpr (DK) dsb[kc][t] = (__bf16)(pr * (dpt[jj] - ds[jj >> 2][jj & 3]));
         }
-      }
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc) {
 #pragma unroll
@@ -608,7 +636,8 @@ static hipError_t launch_bwd_d(const BwdParams& p, const Geometry& gq, const Geo
   pq.ng = gq.ng;
   pq.n_hg = gq.n_hg;
   if (items_q > 0)
-    hipLaunchKernelGGL(bwd_dq_kernel<D>, dim3((unsigned)(items_q * gq.n_hg)), dim3(64 * kBwdWaves), 0, stream, pq);
+    hipLaunchKernelGGL(bwd_dq_kernel<D>, dim3((unsigned)(items_q * gq.n_hg)), dim3(64 * bwd_q_waves(D)), 0, stream,
+                       pq);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   BwdParams pk = p;

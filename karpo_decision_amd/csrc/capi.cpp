@@ -273,7 +273,7 @@ struct BwdSizes {
 
 BwdSizes bwd_sizes_of(const KarpoAttnBwdArgs* b) {
   const KarpoAttnArgs* a = &b->fwd;
-  const Geometry gq = bwd_geometry(a->heads, a->kv_heads, false);
+  const Geometry gq = bwd_geometry(a->heads, a->kv_heads, a->head_dim, false);
   BwdSizes z;
   z.tiles_q = tile_capacity(a, gq);
   z.tiles_k = (a->total_k + 32 * kBwdWaves - 1) / (32 * kBwdWaves) + a->n_seq;
@@ -330,14 +330,14 @@ extern "C" int karpo_attn_bwd(const KarpoAttnBwdArgs* b, void* stream) {
     if (!check_stride(s)) return KARPO_ATTN_ERR_LAYOUT;
   // a step's rows (32 keys, or 32 query rows) are addressed with 32-bit byte offsets
   const int64_t d = a->head_dim;
-  if ((a->k_stride_tok + d) * kBwdStep * 2 >= (int64_t)INT32_MAX ||
-      (a->v_stride_tok + d) * kBwdStep * 2 >= (int64_t)INT32_MAX ||
+  if ((a->k_stride_tok + d) * bwd_q_step(a->head_dim) * 2 >= (int64_t)INT32_MAX ||
+      (a->v_stride_tok + d) * bwd_q_step(a->head_dim) * 2 >= (int64_t)INT32_MAX ||
       (a->q_stride_tok + d) * kBwdStep * 2 >= (int64_t)INT32_MAX ||
       (b->d_o_stride_tok + d) * kBwdStep * 2 >= (int64_t)INT32_MAX || (a->total_q + kBwdStep) * 4 >= INT32_MAX)
     return KARPO_ATTN_ERR_LAYOUT;
   const BwdSizes z = bwd_sizes_of(b);
-  const Geometry gq = bwd_geometry(a->heads, a->kv_heads, false);
-  const Geometry gk = bwd_geometry(a->heads, a->kv_heads, true);
+  const Geometry gq = bwd_geometry(a->heads, a->kv_heads, a->head_dim, false);
+  const Geometry gk = bwd_geometry(a->heads, a->kv_heads, a->head_dim, true);
   if (z.tiles_q * gq.n_hg > (int64_t)INT32_MAX || z.tiles_k * gk.n_hg > (int64_t)INT32_MAX ||
       z.plan_k + kPlanHeader + kItemInts * z.tiles_k > (int64_t)INT32_MAX)
     return KARPO_ATTN_ERR_ARG;

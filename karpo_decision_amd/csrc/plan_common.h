@@ -131,18 +131,28 @@ KA_HD inline int part_cost(int64_t steps, int parts) {
 KA_HD inline int64_t split_slots(const Geometry& g) { return 2 * (int64_t)g.conc / g.n_hg; }
 KA_HD inline int64_t split_tiles(const Geometry& g) { return split_slots(g) / 2; }
 
-// Backward tiles (attn_bwd.hip): four waves of 32 query vectors (dq kernel) or 32 keys (dkdv kernel), 32 keys or
-// query rows per step, never split (conc 1 makes the split length the whole pack).
+// Backward tiles (attn_bwd.hip), never split (conc 1 makes the split length the whole pack):
+//   * dkdv kernel: four waves of 32 keys, 32 query rows per step;
+//   * dq kernel: four waves of 32 query vectors, 32 keys per step (eight waves with 64-key steps, which the kernel
+//     also takes up to head size 128, measured no faster: the step's fixed costs are not what bounds it).
 constexpr int kBwdWaves = 4;
 constexpr int kBwdStep = 32;
+#ifndef KA_BWD_WQ
+#define KA_BWD_WQ 4
+#endif
+#ifndef KA_BWD_BNQ
+#define KA_BWD_BNQ 32
+#endif
+KA_HD constexpr int bwd_q_waves(int head_dim) { return head_dim <= 128 ? KA_BWD_WQ : 4; }
+KA_HD constexpr int bwd_q_step(int head_dim) { return head_dim <= 128 ? KA_BWD_BNQ : 32; }
 // The dq kernel's query tiles (heads grouped as the forward groups them) and the dkdv kernel's key tiles (one
 // key/value head per item; the planner sees keys as queries and query rows as keys).
-KA_HD inline Geometry bwd_geometry(int heads, int kv_heads, bool key_tiles) {
+KA_HD inline Geometry bwd_geometry(int heads, int kv_heads, int head_dim, bool key_tiles) {
   Geometry g;
   g.narrow = false;
-  g.waves = kBwdWaves;
-  g.vectors = 32 * kBwdWaves;
-  g.bn = kBwdStep;
+  g.waves = key_tiles ? kBwdWaves : bwd_q_waves(head_dim);
+  g.vectors = 32 * g.waves;
+  g.bn = key_tiles ? kBwdStep : bwd_q_step(head_dim);
   const int group = heads / kv_heads;
   g.ng = key_tiles ? 1 : (g.vectors % group == 0 ? group : 1);
   g.rows = g.vectors / g.ng;
