@@ -443,28 +443,31 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::template occ_k<MODE>()) 
     qv_off[r] = (uint32_t)(row * p.sq_t + colm) * 2u;
     ov_off[r] = (uint32_t)(row * p.sdo_t + colm) * 2u;
   }
-  // step s: head kvh * group + s / n_rsteps, rows r_first + (s % n_rsteps) * BQ ..
-  const int r_end = r_first + n_rsteps * BQ;
+  // Steps visit the row steps of head kvh * group from the last (r_last) down to r_first, then the group's next
+  // head's. Downwards: under a causal mask every key tile's rows end at the sequence's end, so the tiles that run at
+  // once read the same Q / dO rows at about the same time (L2 hits) instead of rows a tile apart. The copy cursor
+  // moves by pointer increments (no per-step address recomputation).
+  const int r_last = r_first + (n_rsteps - 1) * BQ;
   const int h0 = kvh * p.group;
   const int64_t q_step = (int64_t)BQ * p.sq_t, o_step = (int64_t)BQ * p.sdo_t;
-  const int64_t q_wrap = p.sq_h - n_rsteps * q_step, o_wrap = p.sdo_h - n_rsteps * o_step;
-  const int64_t st_wrap = 2 * p.total_q - (int64_t)n_rsteps * BQ;
-  int c_r0 = r_first;
-  const uint16_t* c_q = p.q + (int64_t)(qa + r_first) * p.sq_t + (int64_t)h0 * p.sq_h;
-  const uint16_t* c_o = p.dout + (int64_t)(qa + r_first) * p.sdo_t + (int64_t)h0 * p.sdo_h;
-  const float* c_st = p.stats + (int64_t)h0 * 2 * p.total_q + qa + r_first;
+  const int64_t q_wrap = p.sq_h + n_rsteps * q_step, o_wrap = p.sdo_h + n_rsteps * o_step;
+  const int64_t st_wrap = 2 * p.total_q + (int64_t)n_rsteps * BQ;
+  int c_r0 = r_last;
+  const uint16_t* c_q = p.q + (int64_t)(qa + r_last) * p.sq_t + (int64_t)h0 * p.sq_h;
+  const uint16_t* c_o = p.dout + (int64_t)(qa + r_last) * p.sdo_t + (int64_t)h0 * p.sdo_h;
+  const float* c_st = p.stats + (int64_t)h0 * 2 * p.total_q + qa + r_last;
   auto copy_step = [&](int s, KA_LDS char* tqk, KA_LDS char* tqv, KA_LDS char* tok, KA_LDS char* tov,
                        KA_LDS float* tst) {
     const int rows = min(lq - c_r0, BQ);
     const uint16_t* qs = c_q;
     const uint16_t* os = c_o;
     const float* src = c_st;
-    c_r0 += BQ;
-    c_q += q_step;
-    c_o += o_step;
-    c_st += BQ;
-    if (c_r0 == r_end) {
-      c_r0 = r_first;
+    c_r0 -= BQ;
+    c_q -= q_step;
+    c_o -= o_step;
+    c_st -= BQ;
+    if (c_r0 < r_first) {  // the group's next head
+      c_r0 = r_last;
       c_q += q_wrap;
       c_o += o_wrap;
       c_st += st_wrap;
@@ -508,7 +511,7 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::template occ_k<MODE>()) 
   KA_LDS char* const tov1 = (KA_LDS char*)ov1;
   KA_LDS float* const tst0 = (KA_LDS float*)sts0;
   KA_LDS float* const tst1 = (KA_LDS float*)sts1;
-  int r_cur = r_first;
+  int r_cur = r_last;
   if (n_steps > 0) copy_step(0, tqk0, tqv0, tok0, tov0, tst0);
   wait_vmcnt<0>();
   __syncthreads();
@@ -518,7 +521,7 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::template occ_k<MODE>()) 
                   KA_LDS char* nok, KA_LDS char* nov, KA_LDS float* nst) {
     if (s + 1 < n_steps) copy_step(s + 1, nqk, nqv, nok, nov, nst);
     const int r0 = r_cur;
-    r_cur = r_cur + BQ == r_end ? r_first : r_cur + BQ;
+    r_cur = r_cur == r_first ? r_last : r_cur - BQ;
     if (r0 < whi && r0 + BQ > wlo) {
       f32x16 st = f32x16{}, dpt = f32x16{};
 #pragma unroll
