@@ -19,11 +19,16 @@ def attend(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, q_cu: to
            plan: ops.Plan | None = None, rows: torch.Tensor | None = None) -> torch.Tensor:
     """(T, heads, D) queries over (Tk, kv heads, D) keys and values (``q_cu`` / ``k_cu``: int32 boundaries), each
     query seeing at most ``window`` keys before its own position; ``rows``: the block plan's ``s_rows`` gather read
-    in place (key row r is row rows[r] of ``key`` / ``value``); (T, heads, D). Forward only: RuntimeError when
-    autograd would need a backward."""
-    if torch.is_grad_enabled() and any(t.requires_grad for t in (query, key, value)):
-        raise RuntimeError("sliding_attention on MI355X runs the forward only (no backward kernel)")
+    in place (key row r is row rows[r] of ``key`` / ``value``); (T, heads, D).
+
+    Differentiable like the reference's FA4 operator pair (sliding_attention.py:36-66): when autograd needs
+    gradients the forward also keeps its log-sum-exp and the backward runs ``karpo_attn_bwd`` (head sizes 64, 128,
+    256; keys and values as tensors, not through ``rows``)."""
     if window < 0:
         raise ValueError(f"a sliding window needs a non-negative left size, not {window}")
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (query, key, value)):
+        if rows is not None:
+            raise ValueError("gradients need the gathered keys and values as tensors (index_select first), not rows")
+        return ops.attention(query, key, value, q_cu, k_cu, max_q, scale, window, 0, spans)
     return ops.run(query, key, value, q_cu, k_cu, max_q, scale, window_left=window, window_right=0, spans=spans,
                    plan=plan, key_rows=rows)

@@ -148,3 +148,48 @@ def test_many_key_tiles_take_the_two_launch_path(gpu):
         r = rel(x, w)
         print(name, f"rel {r:.2e}", flush=True)
         assert r < REL_FRO, (name, r)
+
+
+def test_sliding_attend_trains(gpu):
+    """sliding_attention.attend under autograd (the reference's FA4 operator pair): gradients of a windowed pack with
+    an image span against the oracle; a row table with gradients is refused."""
+    from karpo_decision_amd import sliding_attention
+
+    q, k, v, do, q_cu, k_cu, spans = make_pack([300, 150], [340, 150], 8, 4, 256, seed=41, spans_local=[(0, 20, 60)])
+    dev = torch.device("cuda")
+    xs = [t.to(dev).requires_grad_(True) for t in (q, k, v)]
+    qc, kc = (torch.tensor(x, dtype=torch.int32, device=dev) for x in (q_cu, k_cu))
+    sp = torch.tensor(spans, dtype=torch.int32, device=dev)
+    out = sliding_attention.attend(*xs, qc, kc, 300, 340, 0.0625, 63, spans=sp)
+    out.backward(do.to(dev))
+    want = oa.packed_grads(q, k, v, do, q_cu, k_cu, 0.0625, 63, 0, spans, dtype=torch.float32)
+    for name, x, w in zip(("out", "dq", "dk", "dv"), [out.detach()] + [x.grad for x in xs], want):
+        r = rel(x, w)
+        print("sliding", name, f"rel {r:.2e}", flush=True)
+        assert r < REL_FRO, (name, r)
+    with pytest.raises(ValueError, match="rows"):
+        sliding_attention.attend(*xs, qc, kc, 300, 340, 0.0625, 63, rows=torch.arange(490, device=dev))
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_global_attend_one_sequence_trains(gpu, causal):
+    """global_attention.attend (one virtual sequence, lengths on the device, the reference's cuDNN pair): a branch's
+    queries over its shared keys plus its own, forward without grad and gradients with it, against the oracle."""
+    from karpo_decision_amd import global_attention
+
+    q, k, v, do, q_cu, k_cu, _ = make_pack([200], [520], 8, 2, 128, seed=43)
+    dev = torch.device("cuda")
+    lens = global_attention.lengths(q_cu, k_cu, dev)
+    right = 0 if causal else -1
+    with torch.no_grad():
+        plain = global_attention.attend(q.to(dev), k.to(dev), v.to(dev), lens[0, 0, :1], lens[0, 1, :1], causal,
+                                        0.1)
+    xs = [t.to(dev).requires_grad_(True) for t in (q, k, v)]
+    out = global_attention.attend(*xs, lens[0, 0, :1], lens[0, 1, :1], causal, 0.1)
+    out.backward(do.to(dev))
+    want = oa.packed_grads(q, k, v, do, q_cu, k_cu, 0.1, -1, right, dtype=torch.float32)
+    assert rel(plain, want[0]) < REL_FRO
+    for name, x, w in zip(("out", "dq", "dk", "dv"), [out.detach()] + [x.grad for x in xs], want):
+        r = rel(x, w)
+        print("global", causal, name, f"rel {r:.2e}", flush=True)
+        assert r < REL_FRO, (name, r)
