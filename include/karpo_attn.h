@@ -145,7 +145,8 @@ int karpo_attn_norm_rope(const KarpoNormRopeArgs* args, void* stream);
  * d_q = scale * dS K, d_k = scale * dS^T Q (summed over each key/value head's query heads), d_v = P^T d_o, with
  * P = exp(scale * q.k - lse) over the visible keys and dS = P * (d_o . v - rowsum(d_o * o)). Head sizes 64, 128 and
  * 256; no plan, no row table, no prologue or gate in fwd (their gradients are other ops'). Gradient tensors are bf16
- * with head_dim contiguous; every element of d_q, d_k and d_v is written. */
+ * with head_dim contiguous; every row inside the sequences' bounds (q_cu, k_cu) is written, rows outside them are
+ * not. Deterministic: a key/value head's gradients sum over its query heads in a fixed order (no atomics). */
 typedef struct KarpoAttnBwdArgs {
   KarpoAttnArgs fwd;            /* the forward call's arguments (o = its output); fwd.total_k = rows of k and v;
                                    fwd.workspace / workspace_bytes: karpo_attn_bwd_workspace_bytes of these args */

@@ -203,6 +203,54 @@ def test_fwd_refuses_before_launch(change, status):
     assert _lib.message(status)
 
 
+def _bwd_args(fwd=None, **kw):
+    b = _lib.KarpoAttnBwdArgs()
+    b.fwd = fwd if fwd is not None else _args(total_k=100)
+    b.d_o = b.d_q = b.d_k = b.d_v = 1 << 20  # never dereferenced: every case below is refused before a launch
+    b.lse = 1 << 23
+    b.d_o_stride_tok, b.d_o_stride_head = 256, 64
+    b.d_q_stride_tok, b.d_q_stride_head = 256, 64
+    b.d_k_stride_tok, b.d_k_stride_head = 128, 64
+    b.d_v_stride_tok, b.d_v_stride_head = 128, 64
+    for name, value in kw.items():
+        setattr(b, name, value)
+    return b
+
+
+@pytest.mark.parametrize("change,fwd_change,status", [
+    ({}, dict(head_dim=512), _lib.ERR_HEAD_DIM),  # no backward kernel at 512
+    ({}, dict(head_dim=96), _lib.ERR_HEAD_DIM),
+    ({}, dict(plan=1 << 22), _lib.ERR_ARG),  # the backward plans on the device
+    ({}, dict(k_rows=1 << 22), _lib.ERR_ARG),  # no gathered keys
+    ({}, dict(q_norm=1), _lib.ERR_ARG),  # no prologue
+    ({}, dict(gate=1 << 22), _lib.ERR_ARG),
+    ({}, dict(total_k=0), _lib.ERR_ARG),
+    (dict(lse=0), {}, 1),
+    (dict(d_k=0), {}, 1),
+    (dict(d_o=(1 << 20) + 8), {}, _lib.ERR_LAYOUT),
+    (dict(lse=(1 << 23) + 2), {}, _lib.ERR_LAYOUT),
+    (dict(d_v_stride_tok=130), {}, _lib.ERR_LAYOUT),
+    ({}, {}, 5),  # no workspace
+])
+def test_bwd_refuses_before_launch(change, fwd_change, status):
+    lib = _lib.load()
+    b = _bwd_args(_args(**{"total_k": 100, **fwd_change}), **change)
+    assert lib.karpo_attn_bwd(ctypes.byref(b), None) == status
+    assert _lib.message(status)
+
+
+def test_bwd_workspace_holds_stats_and_both_plans():
+    lib = _lib.load()
+    b = _bwd_args(_args(n_seq=3, total_q=1000, max_q=600, total_k=1500))
+    size = ctypes.c_size_t()
+    assert lib.karpo_attn_bwd_workspace_bytes(ctypes.byref(b), ctypes.byref(size)) == 0
+    stats = 4 * 2 * 1000 * 4  # [heads][2][total_q] fp32
+    tiles_q = min(-(-1000 // 64) + 3, 3 * -(-600 // 64))  # 128 vectors of 2 heads: 64 rows per query tile
+    tiles_k = -(-1500 // 128) + 3
+    assert size.value >= stats + 4 * (8 + 4 * tiles_q + 8 + 4 * tiles_k + 4) and size.value % 256 == 0
+    assert lib.karpo_attn_bwd(ctypes.byref(_bwd_args(_args(total_q=0, total_k=100))), None) == 0  # nothing to do
+
+
 def test_empty_pack_is_a_no_op():
     lib = _lib.load()
     assert lib.karpo_attn_fwd(ctypes.byref(_args(total_q=0)), None) == 0
