@@ -143,8 +143,8 @@ int karpo_attn_norm_rope(const KarpoNormRopeArgs* args, void* stream);
 /* The backward pass of karpo_attn_fwd (the reference's backward ops: families/gemma/sliding_attention.py:50-61,
  * families/gemma/global_attention.py:107-118): from the output gradient d_o, the forward's output o and its lse,
  * d_q = scale * dS K, d_k = scale * dS^T Q (summed over each key/value head's query heads), d_v = P^T d_o, with
- * P = exp(scale * q.k - lse) over the visible keys and dS = P * (d_o . v - rowsum(d_o * o)). Head sizes 64, 128 and
- * 256; no plan, no row table, no prologue or gate in fwd (their gradients are other ops'). Gradient tensors are bf16
+ * P = exp(scale * q.k - lse) over the visible keys and dS = P * (d_o . v - rowsum(d_o * o)). Head sizes 64, 128,
+ * 256 and 512; no plan, no row table, no prologue or gate in fwd (their gradients are other ops'). Gradient tensors are bf16
  * with head_dim contiguous; every row inside the sequences' bounds (q_cu, k_cu) is written, rows outside them are
  * not. Deterministic: a key/value head's gradients sum over its query heads in a fixed order (no atomics). */
 typedef struct KarpoAttnBwdArgs {

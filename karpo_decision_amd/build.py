@@ -24,7 +24,7 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-munsafe-fp-atomics", f"-I{INCLUDE}", f"-I{CSRC}",
 ]
-SOURCES = ["attn_fwd.hip", "attn_bwd.hip", "capi.cpp", "plan.cpp"]
+SOURCES = ["attn_fwd.hip", "attn_bwd.hip", "attn_bwd_pair.hip", "capi.cpp", "plan.cpp"]
 
 
 def hipcc() -> str:

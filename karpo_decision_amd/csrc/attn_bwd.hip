@@ -676,6 +676,14 @@ hipError_t launch_bwd(const BwdParams& p, int head_dim, const Geometry& gq, cons
     case 64: return launch_bwd_d<64>(p, gq, gk, plan_q, plan_k, items_q, items_k, stream);
     case 128: return launch_bwd_d<128>(p, gq, gk, plan_q, plan_k, items_q, items_k, stream);
     case 256: return launch_bwd_d<256>(p, gq, gk, plan_q, plan_k, items_q, items_k, stream);
+    case 512: {
+      const int64_t vectors = p.total_q * p.heads;  // one vector per wave of the statistics pass
+      const int64_t blocks = vectors < 4 * 8192 ? (vectors + 3) / 4 : 8192;
+      if (blocks > 0) hipLaunchKernelGGL(bwd_stats_kernel<512>, dim3((unsigned)blocks), dim3(256), 0, stream, p);
+      e = hipGetLastError();
+      if (e != hipSuccess) return e;
+      return launch_bwd_pair(p, gq, gk, plan_q, plan_k, items_q, items_k, stream);
+    }
     default: return hipErrorInvalidValue;
   }
 }

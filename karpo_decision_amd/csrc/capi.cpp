@@ -276,7 +276,8 @@ BwdSizes bwd_sizes_of(const KarpoAttnBwdArgs* b) {
   const Geometry gq = bwd_geometry(a->heads, a->kv_heads, a->head_dim, false);
   BwdSizes z;
   z.tiles_q = tile_capacity(a, gq);
-  z.tiles_k = (a->total_k + 32 * kBwdWaves - 1) / (32 * kBwdWaves) + a->n_seq;
+  const int keys = bwd_tile_vectors(a->head_dim, true);
+  z.tiles_k = (a->total_k + keys - 1) / keys + a->n_seq;
   z.stats_bytes = ((int64_t)a->heads * 2 * a->total_q * 4 + 255) / 256 * 256;
   z.plan_q = 0;
   z.plan_k = kPlanHeader + kItemInts * z.tiles_q;
@@ -290,7 +291,6 @@ int check_bwd(const KarpoAttnBwdArgs* b) {
   const KarpoAttnArgs* a = &b->fwd;
   const int st = check_shape(a);
   if (st != KARPO_ATTN_OK) return st;
-  if (a->head_dim == 512) return KARPO_ATTN_ERR_HEAD_DIM;
   if (a->total_k < 0) return KARPO_ATTN_ERR_ARG;
   return KARPO_ATTN_OK;
 }

@@ -67,6 +67,9 @@ struct BwdParams {
   float c;      // scale * log2(e) (signed)
   float scale;  // the logit scale (signed): dq and dk carry it
 };
+// Head size 512: the dQ and dK / dV kernels of wave pairs (attn_bwd_pair.hip), after the statistics pass.
+hipError_t launch_bwd_pair(const BwdParams& p, const Geometry& gq, const Geometry& gk, int32_t* plan_q,
+                           int32_t* plan_k, int64_t items_q, int64_t items_k, hipStream_t stream);
 hipError_t launch_bwd(const BwdParams& p, int head_dim, const Geometry& gq, const Geometry& gk, int32_t* plan_q,
                       int32_t* plan_k, int64_t items_q, int64_t items_k, int tiles_q, int merges_q, int tiles_k,
                       int merges_k, int32_t* tile_base, int n_seq, hipStream_t stream);

@@ -145,13 +145,17 @@ constexpr int kBwdStep = 32;
 #endif
 KA_HD constexpr int bwd_q_waves(int head_dim) { return head_dim <= 128 ? KA_BWD_WQ : 4; }
 KA_HD constexpr int bwd_q_step(int head_dim) { return head_dim <= 128 ? KA_BWD_BNQ : 32; }
+// At head size 512 two waves share 32 query vectors or 32 keys (each holds half of D): 64 per four-wave tile.
+KA_HD constexpr int bwd_tile_vectors(int head_dim, bool key_tiles) {
+  return 32 * (key_tiles ? kBwdWaves : bwd_q_waves(head_dim)) / (head_dim == 512 ? 2 : 1);
+}
 // The dq kernel's query tiles (heads grouped as the forward groups them) and the dkdv kernel's key tiles (one
 // key/value head per item; the planner sees keys as queries and query rows as keys).
 KA_HD inline Geometry bwd_geometry(int heads, int kv_heads, int head_dim, bool key_tiles) {
   Geometry g;
   g.narrow = false;
   g.waves = key_tiles ? kBwdWaves : bwd_q_waves(head_dim);
-  g.vectors = 32 * g.waves;
+  g.vectors = bwd_tile_vectors(head_dim, key_tiles);
   g.bn = key_tiles ? kBwdStep : bwd_q_step(head_dim);
   const int group = heads / kv_heads;
   g.ng = key_tiles ? 1 : (g.vectors % group == 0 ? group : 1);

@@ -17,7 +17,7 @@ import torch
 
 from . import ops
 
-#: Head sizes the forward takes; the backward takes 64, 128 and 256.
+#: Head sizes the forward and the backward take (512: the 31B global layers).
 HEADS = (64, 128, 256, 512)
 
 
@@ -39,7 +39,7 @@ def attend(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, q_len: t
            causal: bool, scale: float) -> torch.Tensor:
     """One virtual sequence: (Lq, heads, D) queries over (Lk, kv heads, D) keys and values, ``q_len`` / ``k_len``
     their lengths on the device (``lengths(...)[i, 0, :1]``, ``[i, 1, :1]``); (Lq, heads, D). Gradients flow to
-    query, key and value (head sizes up to 256)."""
+    query, key and value."""
     zero = torch.zeros(1, dtype=torch.int32, device=query.device)
     q_cu = torch.cat([zero, q_len.reshape(-1)[:1].to(torch.int32)])
     k_cu = torch.cat([zero, k_len.reshape(-1)[:1].to(torch.int32)])

@@ -430,9 +430,7 @@ packed_attention_lse.register_autograd(_gradient, setup_context=_setup)
 
 def attention(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_cu: Tensor, max_q: int, scale: float,
               window_left: int = -1, window_right: int = -1, spans: Tensor | None = None) -> Tensor:
-    """The differentiable packed attention (head sizes 64, 128 and 256): (Tq, heads, D) bf16; gradients flow to
-    query, key and value through ``karpo_attn_bwd``."""
-    if query.shape[2] not in (64, 128, 256):
-        raise ValueError(f"the backward takes head sizes 64, 128 and 256, not {query.shape[2]}")
+    """The differentiable packed attention: (Tq, heads, D) bf16; gradients flow to query, key and value through
+    ``karpo_attn_bwd``."""
     return packed_attention_lse(query, key, value, q_cu, k_cu, int(max_q), float(scale), int(window_left),
                                 int(window_right), spans)[0]

@@ -22,8 +22,8 @@ def attend(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, q_cu: to
     in place (key row r is row rows[r] of ``key`` / ``value``); (T, heads, D).
 
     Differentiable like the reference's FA4 operator pair (sliding_attention.py:36-66): when autograd needs
-    gradients the forward also keeps its log-sum-exp and the backward runs ``karpo_attn_bwd`` (head sizes 64, 128,
-    256; keys and values as tensors, not through ``rows``)."""
+    gradients the forward also keeps its log-sum-exp and the backward runs ``karpo_attn_bwd`` (keys and values as
+    tensors, not through ``rows``)."""
     if window < 0:
         raise ValueError(f"a sliding window needs a non-negative left size, not {window}")
     if torch.is_grad_enabled() and any(t.requires_grad for t in (query, key, value)):

@@ -65,6 +65,9 @@ LAYOUTS = [
     ([129, 77], [129, 77], 6, 2, 128, -1, 0, [], None),                  # group 3 does not divide a tile
     ([100], [130], 4, 2, 128, 31, 0, [], -0.09),                         # negative scale, window, branch
     ([96, 64], [96, 64], 4, 2, 256, -1, 0, [(1, 8, 40)], None),
+    ([300, 1, 0, 130], [300, 1, 0, 130], 8, 1, 512, -1, 0, [], None),   # head size 512: wave pairs
+    ([64, 100], [200, 100], 8, 2, 512, -1, 0, [(1, 10, 40)], None),      # branches and a span at 512
+    ([40, 70], [20, 70], 4, 4, 512, 31, 0, [], -0.05),                  # Lq > Lk, window, negative scale at 512
 ]
 
 
@@ -128,10 +131,9 @@ def test_backward_is_deterministic(gpu):
 
 def test_backward_refuses_what_it_does_not_take(gpu):
     dev = torch.device("cuda")
-    q = torch.randn(8, 2, 512, device=dev).bfloat16()
     cu = torch.tensor([0, 8], dtype=torch.int32, device=dev)
     with pytest.raises(ValueError):
-        ops.attention(q, q, q, cu, cu, 8, 0.1)
+        ops.attention(*(torch.randn(8, 2, 96, device=dev).bfloat16(),) * 3, cu, cu, 8, 0.1)
     q = torch.randn(8, 2, 64, device=dev).bfloat16()
     out, lse = ops.packed_attention_lse(q, q, q, cu, cu, 8, 0.1, -1, 0, None)
     with pytest.raises(ValueError):
@@ -193,3 +195,26 @@ def test_global_attend_one_sequence_trains(gpu, causal):
         r = rel(x, w)
         print("global", causal, name, f"rel {r:.2e}", flush=True)
         assert r < REL_FRO, (name, r)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_head_512_one_sequence_cases_of_the_reference(gpu, causal):
+    """The reference's cuDNN backward cases (tests/gpu/test_packed_gemma.py:145-184: (Lq, Lk) pairs at head size 512,
+    causal and bidirectional) through global_attention.attend, at 8 / 4 heads (the kernel's work per head is the
+    reference's 32 / 16), against the oracle's float32 gradients."""
+    from karpo_decision_amd import global_attention
+
+    dev = torch.device("cuda")
+    for n, (lq, lk) in enumerate([(700, 1900), (1500, 1500), (333, 2047), (37, 4100), (4097, 4097), (900, 9000),
+                                  (256, 256)]):
+        q, k, v, do, q_cu, k_cu, _ = make_pack([lq], [lk], 8, 4, 512, seed=50 + n)
+        lens = global_attention.lengths(q_cu, k_cu, dev)
+        xs = [t.to(dev).requires_grad_(True) for t in (q, k, v)]
+        out = global_attention.attend(*xs, lens[0, 0, :1], lens[0, 1, :1], causal, 1.0 / 16)
+        out.backward(do.to(dev))
+        torch.cuda.synchronize()
+        want = oa.packed_grads(q, k, v, do, q_cu, k_cu, 1.0 / 16, -1, 0 if causal else -1, dtype=torch.float32)
+        for name, x, w in zip(("out", "dq", "dk", "dv"), [out.detach()] + [x.grad for x in xs], want):
+            r = rel(x, w)
+            print((lq, lk), causal, name, f"rel {r:.2e}", flush=True)
+            assert r < REL_FRO, ((lq, lk), name, r)

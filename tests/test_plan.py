@@ -218,7 +218,6 @@ def _bwd_args(fwd=None, **kw):
 
 
 @pytest.mark.parametrize("change,fwd_change,status", [
-    ({}, dict(head_dim=512), _lib.ERR_HEAD_DIM),  # no backward kernel at 512
     ({}, dict(head_dim=96), _lib.ERR_HEAD_DIM),
     ({}, dict(plan=1 << 22), _lib.ERR_ARG),  # the backward plans on the device
     ({}, dict(k_rows=1 << 22), _lib.ERR_ARG),  # no gathered keys
