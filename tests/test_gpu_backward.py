@@ -218,3 +218,29 @@ def test_head_512_one_sequence_cases_of_the_reference(gpu, causal):
             r = rel(x, w)
             print((lq, lk), causal, name, f"rel {r:.2e}", flush=True)
             assert r < REL_FRO, ((lq, lk), name, r)
+
+
+def test_sliding_case_of_the_reference(gpu):
+    """The reference's FA4 sliding test (tests/gpu/test_packed_gemma.py:70-104): head size 256, 32 / 16 heads, window
+    1023, queries and keys with their own bounds (three branches after a shared tail), loss sum(out * linspace(-1, 1));
+    output and gradients within the reference's floor (relative 5e-3) of float32."""
+    from karpo_decision_amd import sliding_attention
+
+    q_len = [1500, 120, 300, 1023, 1024, 1025, 40, 2500, 7]
+    k_len = [1500, 1143, 1323, 1023, 1024, 1025, 40, 2500, 1030]
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (torch.randn(sum(n), h, 256, generator=g).bfloat16() for n, h in ((q_len, 32), (k_len, 16), (k_len, 16)))
+    q_cu = np.concatenate([[0], np.cumsum(q_len)]).astype(int).tolist()
+    k_cu = np.concatenate([[0], np.cumsum(k_len)]).astype(int).tolist()
+    dev = torch.device("cuda")
+    xs = [t.to(dev).requires_grad_(True) for t in (q, k, v)]
+    qc, kc = (torch.tensor(x, dtype=torch.int32, device=dev) for x in (q_cu, k_cu))
+    out = sliding_attention.attend(*xs, qc, kc, max(q_len), max(k_len), 256 ** -0.5, 1023)
+    weight = torch.linspace(-1, 1, out.numel(), device=dev).view_as(out)
+    (out.float() * weight).sum().backward()
+    torch.cuda.synchronize()
+    want = oa.packed_grads(q, k, v, weight.cpu(), q_cu, k_cu, 256 ** -0.5, 1023, 0, dtype=torch.float32)
+    for name, x, w in zip(("out", "dq", "dk", "dv"), [out.detach()] + [x.grad for x in xs], want):
+        r = rel(x, w)
+        print("reference sliding case", name, f"rel {r:.2e}", flush=True)
+        assert r < 5e-3, (name, r)
