@@ -86,11 +86,9 @@ __global__ __launch_bounds__(64 * bwd_q_waves(D), BwdCfg<D>::BLOCKS_Q) void bwd_
   constexpr int W = bwd_q_waves(D), BN = bwd_q_step(D), KB = BN / 32;
   constexpr int DC = D / 16, DB = D / 32, KC = BN / 16;
   constexpr int TILE = BN * D * 2, BLKS = TILE / 1024, INSTS = (BLKS + W - 1) / W;
-  __shared__ __attribute__((aligned(1024))) char kk0[TILE];  // K, row-operand layout
+  __shared__ __attribute__((aligned(1024))) char kk0[TILE];  // K (S layout: read as rows and transposed)
   __shared__ __attribute__((aligned(1024))) char kk1[TILE];
-  __shared__ __attribute__((aligned(1024))) char kv0[TILE];  // K, transposed-read layout
-  __shared__ __attribute__((aligned(1024))) char kv1[TILE];
-  __shared__ __attribute__((aligned(1024))) char vk0[TILE];  // V, row-operand layout
+  __shared__ __attribute__((aligned(1024))) char vk0[TILE];  // V (S layout, read as rows)
   __shared__ __attribute__((aligned(1024))) char vk1[TILE];
   __shared__ int red[2][W];
 
@@ -190,23 +188,21 @@ __global__ __launch_bounds__(64 * bwd_q_waves(D), BwdCfg<D>::BLOCKS_Q) void bwd_
   const int j_first = klo < khi ? (klo / BN) * BN : 0;
   const int n_steps = klo < khi ? (khi - j_first + BN - 1) / BN : 0;
 
-  // copies: K into both layouts, V into the row-operand layout (zeros past the sequence's last key)
+  // copies: K and V in the S layout (zeros past the sequence's last key)
   const uint16_t* kbase = p.k + (int64_t)kvh * p.sk_h + (int64_t)ka * p.sk_t;
   const uint16_t* vbase = p.v + (int64_t)kvh * p.sv_h + (int64_t)ka * p.sv_t;
-  uint32_t kk_off[INSTS], kv_off[INSTS], vk_off[INSTS];
+  uint32_t kk_off[INSTS], vk_off[INSTS];
 #pragma unroll
   for (int r = 0; r < INSTS; ++r) {
     int key, colm;
-    k_dma_source<D>(wave * INSTS + r, lane, &key, &colm);
+    s_dma_source<D>(wave * INSTS + r, lane, &key, &colm);
     kk_off[r] = (uint32_t)(key * p.sk_t + colm) * 2u;
     vk_off[r] = (uint32_t)(key * p.sv_t + colm) * 2u;
-    v_dma_source<D>(wave * INSTS + r, lane, &key, &colm);
-    kv_off[r] = (uint32_t)(key * p.sk_t + colm) * 2u;
   }
   const uint16_t* c_k = kbase + (int64_t)j_first * p.sk_t;
   const uint16_t* c_v = vbase + (int64_t)j_first * p.sv_t;
   const int64_t k_step = (int64_t)BN * p.sk_t, v_step = (int64_t)BN * p.sv_t;
-  auto copy_step = [&](int j0, KA_LDS char* tkk, KA_LDS char* tkv, KA_LDS char* tvk) {
+  auto copy_step = [&](int j0, KA_LDS char* tkk, KA_LDS char* tvk) {
     const int rows = min(lk - j0, BN);
     const uint16_t* ks = c_k;
     const uint16_t* vs = c_v;
@@ -217,13 +213,12 @@ __global__ __launch_bounds__(64 * bwd_q_waves(D), BwdCfg<D>::BLOCKS_Q) void bwd_
       if (BLKS % W == 0 || wave * INSTS + r < BLKS) {
         const int at = (wave * INSTS + r) * 1024;
         dma_16b(ks, rows * (int)p.sk_t * 2, tkk + at, kk_off[r]);
-        dma_16b(ks, rows * (int)p.sk_t * 2, tkv + at, kv_off[r]);
         dma_16b(vs, rows * (int)p.sv_t * 2, tvk + at, vk_off[r]);
       }
   };
-  const int k_read = k_offset<D>(key_row(col), half);
-  const int g = lane >> 4, jl = lane & 15;
-  const int v_read = v_offset<D>(8 * (g >> 1) + (jl >> 2), 16 * (g & 1) + 4 * (jl & 3));
+  // row reads of chunk 2 dc + half: k_read[dc & 1] + (dc >> 1) * 1024; transposed reads: t_read[rr] + kc, db offsets
+  const int k_read[2] = {s_offset<D>(key_row(col), half), s_offset<D>(key_row(col), 2 + half)};
+  const int t_read[2] = {s_tr_base(lane, 0), s_tr_base(lane, 1)};
   f32x16 acc[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
@@ -231,18 +226,15 @@ __global__ __launch_bounds__(64 * bwd_q_waves(D), BwdCfg<D>::BLOCKS_Q) void bwd_
 
   KA_LDS char* const tkk0 = (KA_LDS char*)kk0;
   KA_LDS char* const tkk1 = (KA_LDS char*)kk1;
-  KA_LDS char* const tkv0 = (KA_LDS char*)kv0;
-  KA_LDS char* const tkv1 = (KA_LDS char*)kv1;
   KA_LDS char* const tvk0 = (KA_LDS char*)vk0;
   KA_LDS char* const tvk1 = (KA_LDS char*)vk1;
-  if (n_steps > 0) copy_step(j_first, tkk0, tkv0, tvk0);
+  if (n_steps > 0) copy_step(j_first, tkk0, tvk0);
   wait_vmcnt<0>();
   __syncthreads();
 
-  auto step = [&](int s, const KA_LDS char* tkk, const KA_LDS char* tkv, const KA_LDS char* tvk, KA_LDS char* nkk,
-                  KA_LDS char* nkv, KA_LDS char* nvk) {
+  auto step = [&](int s, const KA_LDS char* tkk, const KA_LDS char* tvk, KA_LDS char* nkk, KA_LDS char* nvk) {
     const int j0 = j_first + s * BN;
-    if (s + 1 < n_steps) copy_step(j0 + BN, nkk, nkv, nvk);
+    if (s + 1 < n_steps) copy_step(j0 + BN, nkk, nvk);
     if (j0 < whi && j0 + BN > wlo) {
       f32x16 st[KB], dpt[KB];
 #pragma unroll
@@ -254,7 +246,7 @@ __global__ __launch_bounds__(64 * bwd_q_waves(D), BwdCfg<D>::BLOCKS_Q) void bwd_
       for (int dc = 0; dc < DC; ++dc) {
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {  // key block kb: rows kb * 32 .. of the step
-          const int at = k_read + kb * (2 * (D / 8) * 256) + dc * 512;
+          const int at = k_read[dc & 1] + (dc >> 1) * 1024 + kb * (2 * (D / 8) * 256);
           const bf16x8 a = *(const KA_LDS bf16x8*)(tkk + at);
           st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qop[dc], st[kb], 0, 0, 0);
           const bf16x8 b = *(const KA_LDS bf16x8*)(tvk + at);
@@ -294,7 +286,7 @@ __global__ __launch_bounds__(64 * bwd_q_waves(D), BwdCfg<D>::BLOCKS_Q) void bwd_
           for (int rr = 0; rr < 2; ++rr)
             pv[rr] = __builtin_bit_cast(
                 bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                            (KA_LDS s16x4*)(tkv + v_read + (kc * 4 + rr) * (D / 16) * 128 + db * 256)));
+                            (KA_LDS s16x4*)(tkk + t_read[rr] + kc * (D / 8) * 256 + db * 1024)));
           const bf16x8 a = __builtin_shufflevector(pv[0], pv[1], 0, 1, 2, 3, 4, 5, 6, 7);
           acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, dsb[kc], acc[db], 0, 0, 0);
         }
@@ -305,10 +297,10 @@ __global__ __launch_bounds__(64 * bwd_q_waves(D), BwdCfg<D>::BLOCKS_Q) void bwd_
   };
   int s = 0;
   for (; s + 1 < n_steps; s += 2) {
-    step(s, tkk0, tkv0, tvk0, tkk1, tkv1, tvk1);
-    step(s + 1, tkk1, tkv1, tvk1, tkk0, tkv0, tvk0);
+    step(s, tkk0, tvk0, tkk1, tvk1);
+    step(s + 1, tkk1, tvk1, tkk0, tvk0);
   }
-  if (s < n_steps) step(s, tkk0, tkv0, tvk0, tkk1, tkv1, tvk1);
+  if (s < n_steps) step(s, tkk0, tvk0, tkk1, tvk1);
 
   if (valid) {  // dq = scale * acc: lane (col, half) holds d = db*32 + (j/4)*8 + half*4 + j%4
     uint16_t* dp = p.dq + (int64_t)(qa + pos) * p.sdq_t + (int64_t)head * p.sdq_h + half * 4;
@@ -332,14 +324,10 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::template occ_k<MODE>()) 
   constexpr int W = kBwdWaves, BQ = kBwdStep;
   constexpr int DC = D / 16, DB = D / 32, KC = BQ / 16;
   constexpr int TILE = BQ * D * 2, BLKS = TILE / 1024, INSTS = (BLKS + W - 1) / W;
-  __shared__ __attribute__((aligned(1024))) char qk0[TILE];  // Q, row-operand layout
+  __shared__ __attribute__((aligned(1024))) char qk0[TILE];  // Q (S layout: rows for S, transposed for dK)
   __shared__ __attribute__((aligned(1024))) char qk1[TILE];
-  __shared__ __attribute__((aligned(1024))) char qv0[TILE];  // Q, transposed-read layout
-  __shared__ __attribute__((aligned(1024))) char qv1[TILE];
-  __shared__ __attribute__((aligned(1024))) char ok0[TILE];  // dO, row-operand layout
+  __shared__ __attribute__((aligned(1024))) char ok0[TILE];  // dO (S layout: rows for dP, transposed for dV; dV alone: transposed-read layout)
   __shared__ __attribute__((aligned(1024))) char ok1[TILE];
-  __shared__ __attribute__((aligned(1024))) char ov0[TILE];  // dO, transposed-read layout
-  __shared__ __attribute__((aligned(1024))) char ov1[TILE];
   __shared__ __attribute__((aligned(256))) float sts0[2 * BQ];  // log2 LSE, then D, of the step's rows
   __shared__ __attribute__((aligned(256))) float sts1[2 * BQ];
   __shared__ int red[2][W];
@@ -432,16 +420,17 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::template occ_k<MODE>()) 
   const int n_rsteps = qlo < qhi ? (qhi - r_first + BQ - 1) / BQ : 0;
   const int n_steps = n_rsteps * p.group;  // every head of the group in turn
 
-  uint32_t qk_off[INSTS], qv_off[INSTS], ok_off[INSTS], ov_off[INSTS];
+  // dV alone reads dO only transposed: it keeps the transposed-read layout, whose copy reads whole rows (the S
+  // layout's reads 64 bytes of each of 16 rows per instruction)
+  constexpr bool OV = MODE == 1;
+  uint32_t qk_off[INSTS], ok_off[INSTS];
 #pragma unroll
   for (int r = 0; r < INSTS; ++r) {
     int row, colm;
-    k_dma_source<D>(wave * INSTS + r, lane, &row, &colm);
+    s_dma_source<D>(wave * INSTS + r, lane, &row, &colm);
     qk_off[r] = (uint32_t)(row * p.sq_t + colm) * 2u;
+    if constexpr (OV) v_dma_source<D>(wave * INSTS + r, lane, &row, &colm);
     ok_off[r] = (uint32_t)(row * p.sdo_t + colm) * 2u;
-    v_dma_source<D>(wave * INSTS + r, lane, &row, &colm);
-    qv_off[r] = (uint32_t)(row * p.sq_t + colm) * 2u;
-    ov_off[r] = (uint32_t)(row * p.sdo_t + colm) * 2u;
   }
   // Steps visit the row steps of head kvh * group from the last (r_last) down to r_first, then the group's next
   // head's. Downwards: under a causal mask every key tile's rows end at the sequence's end, so the tiles that run at
@@ -456,8 +445,7 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::template occ_k<MODE>()) 
   const uint16_t* c_q = p.q + (int64_t)(qa + r_last) * p.sq_t + (int64_t)h0 * p.sq_h;
   const uint16_t* c_o = p.dout + (int64_t)(qa + r_last) * p.sdo_t + (int64_t)h0 * p.sdo_h;
   const float* c_st = p.stats + (int64_t)h0 * 2 * p.total_q + qa + r_last;
-  auto copy_step = [&](int s, KA_LDS char* tqk, KA_LDS char* tqv, KA_LDS char* tok, KA_LDS char* tov,
-                       KA_LDS float* tst) {
+  auto copy_step = [&](int s, KA_LDS char* tqk, KA_LDS char* tok, KA_LDS float* tst) {
     const int rows = min(lq - c_r0, BQ);
     const uint16_t* qs = c_q;
     const uint16_t* os = c_o;
@@ -477,11 +465,7 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::template occ_k<MODE>()) 
       if (BLKS % W == 0 || wave * INSTS + r < BLKS) {
         const int at = (wave * INSTS + r) * 1024;
         dma_16b(qs, rows * (int)p.sq_t * 2, tqk + at, qk_off[r]);
-        if constexpr (DK) {
-          dma_16b(qs, rows * (int)p.sq_t * 2, tqv + at, qv_off[r]);
-          dma_16b(os, rows * (int)p.sdo_t * 2, tok + at, ok_off[r]);
-        }
-        if constexpr (DV) dma_16b(os, rows * (int)p.sdo_t * 2, tov + at, ov_off[r]);
+        dma_16b(os, rows * (int)p.sdo_t * 2, tok + at, ok_off[r]);
       }
     if (wave == W - 1) {  // 32 log2 LSE (lanes 0-31) then 32 D (lanes 32-63), 4 B per lane; zeros past the stats
       const __amdgpu_buffer_rsrc_t rs =
@@ -490,7 +474,9 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::template occ_k<MODE>()) 
                                                (uint32_t)((lane >> 5) * p.total_q + (lane & 31)) * 4u, 0, 0, 0);
     }
   };
-  const int q_read = k_offset<D>(key_row(col), half);
+  // row reads of chunk 2 dc + half: q_read[dc & 1] + (dc >> 1) * 1024; transposed reads: t_read[rr] + kc, db offsets
+  const int q_read[2] = {s_offset<D>(key_row(col), half), s_offset<D>(key_row(col), 2 + half)};
+  const int t_read[2] = {s_tr_base(lane, 0), s_tr_base(lane, 1)};
   const int g = lane >> 4, jl = lane & 15;
   const int v_read = v_offset<D>(8 * (g >> 1) + (jl >> 2), 16 * (g & 1) + 4 * (jl & 3));
   f32x16 dk[DB], dv[DB];
@@ -503,33 +489,28 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::template occ_k<MODE>()) 
 
   KA_LDS char* const tqk0 = (KA_LDS char*)qk0;
   KA_LDS char* const tqk1 = (KA_LDS char*)qk1;
-  KA_LDS char* const tqv0 = (KA_LDS char*)qv0;
-  KA_LDS char* const tqv1 = (KA_LDS char*)qv1;
   KA_LDS char* const tok0 = (KA_LDS char*)ok0;
   KA_LDS char* const tok1 = (KA_LDS char*)ok1;
-  KA_LDS char* const tov0 = (KA_LDS char*)ov0;
-  KA_LDS char* const tov1 = (KA_LDS char*)ov1;
   KA_LDS float* const tst0 = (KA_LDS float*)sts0;
   KA_LDS float* const tst1 = (KA_LDS float*)sts1;
   int r_cur = r_last;
-  if (n_steps > 0) copy_step(0, tqk0, tqv0, tok0, tov0, tst0);
+  if (n_steps > 0) copy_step(0, tqk0, tok0, tst0);
   wait_vmcnt<0>();
   __syncthreads();
 
-  auto step = [&](int s, const KA_LDS char* tqk, const KA_LDS char* tqv, const KA_LDS char* tok,
-                  const KA_LDS char* tov, const KA_LDS float* tst, KA_LDS char* nqk, KA_LDS char* nqv,
-                  KA_LDS char* nok, KA_LDS char* nov, KA_LDS float* nst) {
-    if (s + 1 < n_steps) copy_step(s + 1, nqk, nqv, nok, nov, nst);
+  auto step = [&](int s, const KA_LDS char* tqk, const KA_LDS char* tok, const KA_LDS float* tst, KA_LDS char* nqk,
+                  KA_LDS char* nok, KA_LDS float* nst) {
+    if (s + 1 < n_steps) copy_step(s + 1, nqk, nok, nst);
     const int r0 = r_cur;
     r_cur = r_cur == r_first ? r_last : r_cur - BQ;
     if (r0 < whi && r0 + BQ > wlo) {
       f32x16 st = f32x16{}, dpt = f32x16{};
 #pragma unroll
       for (int dc = 0; dc < DC; ++dc) {
-        const bf16x8 a = *(const KA_LDS bf16x8*)(tqk + q_read + dc * 512);
+        const bf16x8 a = *(const KA_LDS bf16x8*)(tqk + q_read[dc & 1] + (dc >> 1) * 1024);
         st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, kop[dc], st, 0, 0, 0);
         if constexpr (DK) {
-          const bf16x8 b = *(const KA_LDS bf16x8*)(tok + q_read + dc * 512);
+          const bf16x8 b = *(const KA_LDS bf16x8*)(tok + q_read[dc & 1] + (dc >> 1) * 1024);
           dpt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, vop[dc], dpt, 0, 0, 0);
         }
       }
@@ -572,11 +553,12 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::template occ_k<MODE>()) 
           bf16x4 ov[2], qv[2];
 #pragma unroll
           for (int rr = 0; rr < 2; ++rr) {
-            const int at = v_read + (kc * 4 + rr) * (D / 16) * 128 + db * 256;
+            const int at = t_read[rr] + kc * (D / 8) * 256 + db * 1024;
+            const int vt = OV ? v_read + (kc * 4 + rr) * (D / 16) * 128 + db * 256 : at;
             if constexpr (DV)
-              ov[rr] = __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((KA_LDS s16x4*)(tov + at)));
+              ov[rr] = __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((KA_LDS s16x4*)(tok + vt)));
             if constexpr (DK)
-              qv[rr] = __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((KA_LDS s16x4*)(tqv + at)));
+              qv[rr] = __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((KA_LDS s16x4*)(tqk + at)));
           }
           if constexpr (DV) {
             const bf16x8 ao = __builtin_shufflevector(ov[0], ov[1], 0, 1, 2, 3, 4, 5, 6, 7);
@@ -594,10 +576,10 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::template occ_k<MODE>()) 
   };
   int s = 0;
   for (; s + 1 < n_steps; s += 2) {
-    step(s, tqk0, tqv0, tok0, tov0, tst0, tqk1, tqv1, tok1, tov1, tst1);
-    step(s + 1, tqk1, tqv1, tok1, tov1, tst1, tqk0, tqv0, tok0, tov0, tst0);
+    step(s, tqk0, tok0, tst0, tqk1, tok1, tst1);
+    step(s + 1, tqk1, tok1, tst1, tqk0, tok0, tst0);
   }
-  if (s < n_steps) step(s, tqk0, tqv0, tok0, tov0, tst0, tqk1, tqv1, tok1, tov1, tst1);
+  if (s < n_steps) step(s, tqk0, tok0, tst0, tqk1, tok1, tst1);
 
   if (valid) {  // lane (col, half) holds d = db*32 + (j/4)*8 + half*4 + j%4 of its key
     uint16_t* kq = p.dk + (int64_t)(ka + key) * p.sdk_t + (int64_t)kvh * p.sdk_h + half * 4;

@@ -74,6 +74,33 @@ __device__ __forceinline__ void v_dma_source(int blk, int lane, int* key, int* c
   *col = (b % (D / 16)) * 16 + (piece & 1) * 8;
 }
 
+// The S layout: rows (keys, or query rows) staged once and read both as MFMA row operands (ds_read_b128, one row's
+// 16-byte chunk per lane) and transposed (ds_read_b64_tr_b16, four rows of one column group per lane). Chunk c of
+// row k sits at ((k / 16) * D/8 + c) * 256 + ((k % 16) ^ 4 (c % 4)) * 16: a 256 B run holds 16 rows' chunk c, with the
+// rows' order XOR-swizzled by the chunk index, so the 16 lanes of a row read cover one run and the 32 lanes of a
+// transposed read (four rows x chunks c .. c+3) cover 64 distinct banks.
+template <int D>
+__device__ __forceinline__ int s_offset(int k, int c) {
+  return ((k >> 4) * (D / 8) + c) * 256 + (((k & 15) ^ ((c & 3) << 2)) * 16);
+}
+// Inverse of s_offset for byte offset blk * 1024 + lane * 16 (the copy's source row and first column).
+template <int D>
+__device__ __forceinline__ void s_dma_source(int blk, int lane, int* row, int* col) {
+  const int b = blk * 4 + (lane >> 4);  // 256-byte run: (row block, chunk)
+  const int c = b % (D / 8);
+  *row = (b / (D / 8)) * 16 + ((lane & 15) ^ ((c & 3) << 2));
+  *col = c * 8;
+}
+// Row-operand read of element chunk 2 dc + half of row k: s_offset(k, 2 dc + half) = base[dc & 1] + (dc >> 1) * 1024
+// with base[i] = s_offset(k, 2 i + half).
+// Transposed read (the A operand rows d = db*32 + lane%32 over rows kc*16 + (lane/32)*8 .. +8 of the step, two reads
+// rr = 0, 1 of four rows each): this lane's address is s_tr_base(lane, rr) + kc * (D/8) * 256 + db * 1024.
+__device__ __forceinline__ int s_tr_base(int lane, int rr) {
+  const int g = lane >> 4, jl = lane & 15;
+  const int c = 2 * (g & 1) + ((jl >> 1) & 1);  // chunk within the 32-column block (its index mod 4)
+  return c * 256 + (((4 * rr + 8 * (g >> 1) + (jl >> 2)) ^ (c << 2)) * 16) + (jl & 1) * 8;
+}
+
 // s_waitcnt vmcnt(N) (expcnt and lgkmcnt not waited on): at most N vector-memory operations of this wave in flight.
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
