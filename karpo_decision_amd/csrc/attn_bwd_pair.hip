@@ -6,11 +6,11 @@
 // partials through LDS (low half + high half, in that order in both waves, so both hold bit-equal sums), both run the
 // same softmax, and each accumulates its half of the gradient.
 //
-// LDS holds one stage of a step's tiles (32 rows x 512 bf16 = 32 KiB per layout, three layouts for dQ and dK), so
-// copies are phased within the step instead of double-buffered: the row-operand tiles of step s + 1 are copied while
-// step s runs its softmax and its gradient products (they were last read before the first barrier), and the
-// transposed tile of step s + 1 while step s + 1 runs its S / dP products (it was last read before the third).
-// Three barriers per step.
+// A step has two barriers: (1) after the S / dP products (the partials are written), (2) at its end. The tile a step
+// reads in both halves of the step (K for dQ, Q for dK and dV; S layout, read as rows and transposed) has two
+// buffers: the next step's is copied from the step's start, a whole step ahead of its use. dV's transposed dO has two
+// buffers as well. The row tile read only by the products before barrier 1 (V for dQ, dO for dK) has one buffer,
+// refilled for the next step right after barrier 1. 32 KiB per tile and buffer.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -27,20 +27,20 @@ constexpr int kPairWaves = 4;  // two pairs per workgroup
 constexpr int kPairStep = 32;  // keys (dQ) or query rows (dK, dV) per step
 
 // A wave's eight 1 KiB copy blocks per tile (blocks 8w .. 8w+7 of 32) at head size 512, as byte offsets from the
-// tile's first row (k_dma_source / v_dma_source of block 8w + r): the row-operand layout's advance 64 B per block;
-// the transposed layout's advance 256 B per block, and four rows further from block 4 on. One or two registers per
-// layout instead of eight (checked against the per-block formulas for every wave, lane and block).
-__device__ __forceinline__ uint32_t k_block_base(int wave, int lane, int64_t stride) {
-  int key, colm;
-  k_dma_source<512>(wave * 8, lane, &key, &colm);
-  return (uint32_t)(key * stride + colm) * 2u;
+// tile's first row (s_dma_source / v_dma_source of block 8w + r): the S layout's advance 64 B per block; the
+// transposed layout's advance 256 B per block, and four rows further from block 4 on. One or two registers per layout
+// instead of eight (checked against the per-block formulas for every wave, lane and block).
+__device__ __forceinline__ uint32_t s_block_base(int wave, int lane, int64_t stride) {
+  int row, colm;
+  s_dma_source<512>(wave * 8, lane, &row, &colm);
+  return (uint32_t)(row * stride + colm) * 2u;
 }
 __device__ __forceinline__ uint32_t v_block_base(int wave, int lane, int64_t stride) {
   int key, colm;
   v_dma_source<512>(wave * 8, lane, &key, &colm);
   return (uint32_t)(key * stride + colm) * 2u;
 }
-__device__ __forceinline__ uint32_t k_block(uint32_t base, int r) { return base + (uint32_t)r * 64u; }
+__device__ __forceinline__ uint32_t s_block(uint32_t base, int r) { return base + (uint32_t)r * 64u; }
 __device__ __forceinline__ uint32_t v_block(uint32_t base, int64_t stride, int r) {
   return base + (uint32_t)(r >> 2) * (uint32_t)(8 * stride) + (uint32_t)(r & 3) * 256u;
 }
@@ -83,9 +83,9 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void bwd_dq_pair_kernel(BwdPara
   constexpr int DH = D / 2, QC = DH / 16, OB = DH / 32, KC = BN / 16;
   constexpr int TILE = BN * D * 2, INSTS = TILE / 1024 / W;
   static_assert(INSTS * W * 1024 == TILE, "every wave copies the same number of 1 KiB blocks per tile");
-  __shared__ __attribute__((aligned(1024))) char kk_s[TILE];  // K, row-operand layout
-  __shared__ __attribute__((aligned(1024))) char kv_s[TILE];  // K, transposed-read layout
-  __shared__ __attribute__((aligned(1024))) char vk_s[TILE];  // V, row-operand layout
+  __shared__ __attribute__((aligned(1024))) char k0_s[TILE];  // K of even steps (S layout: rows and transposed)
+  __shared__ __attribute__((aligned(1024))) char k1_s[TILE];  // K of odd steps
+  __shared__ __attribute__((aligned(1024))) char v_s[TILE];   // V (S layout, read as rows)
   __shared__ __attribute__((aligned(16))) f32x4 xch[W][8 * 64];
   __shared__ int red[2][W];
 
@@ -148,42 +148,36 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void bwd_dq_pair_kernel(BwdPara
   const int n_steps = klo < khi ? (khi - j_first + BN - 1) / BN : 0;
 
   static_assert(D == 512 && INSTS == 8, "the block offsets below are those of head size 512");
-  const uint32_t kk_off = k_block_base(wave, lane, p.sk_t), vk_off = k_block_base(wave, lane, p.sv_t);
-  const uint32_t kv_off = v_block_base(wave, lane, p.sk_t);
-  KA_LDS char* const kk = (KA_LDS char*)kk_s;
-  KA_LDS char* const kv = (KA_LDS char*)kv_s;
-  KA_LDS char* const vk = (KA_LDS char*)vk_s;
-  // two copy cursors (the row-operand tiles and the transposed one are copied at different points of a step)
+  const uint32_t k_off = s_block_base(wave, lane, p.sk_t), v_off = s_block_base(wave, lane, p.sv_t);
+  KA_LDS char* const k0 = (KA_LDS char*)k0_s;
+  KA_LDS char* const k1 = (KA_LDS char*)k1_s;
+  KA_LDS char* const vt = (KA_LDS char*)v_s;
+  // copy cursors (K is copied at a step's start, V after its first barrier, both for the next step)
   const int64_t k_step = (int64_t)BN * p.sk_t, v_step = (int64_t)BN * p.sv_t;
-  const uint16_t* kbase = p.k + (int64_t)kvh * p.sk_h + (int64_t)(ka + j_first) * p.sk_t;
-  const uint16_t* vbase = p.v + (int64_t)kvh * p.sv_h + (int64_t)(ka + j_first) * p.sv_t;
-  int r_j0 = j_first, t_j0 = j_first;
-  const uint16_t* r_k = kbase;
-  const uint16_t* r_v = vbase;
-  const uint16_t* t_k = kbase;
-  auto copy_rows = [&]() {
-    const int rows = min(lk - r_j0, BN);
-#pragma unroll
-    for (int r = 0; r < INSTS; ++r) {
-      const int at = (wave * INSTS + r) * 1024;
-      dma_16b(r_k, rows * (int)p.sk_t * 2, kk + at, k_block(kk_off, r));
-      dma_16b(r_v, rows * (int)p.sv_t * 2, vk + at, k_block(vk_off, r));
-    }
-    r_j0 += BN;
-    r_k += k_step;
-    r_v += v_step;
-  };
-  auto copy_trans = [&]() {
-    const int rows = min(lk - t_j0, BN);
+  int ck_j0 = j_first, cv_j0 = j_first;
+  const uint16_t* c_k = p.k + (int64_t)kvh * p.sk_h + (int64_t)(ka + j_first) * p.sk_t;
+  const uint16_t* c_v = p.v + (int64_t)kvh * p.sv_h + (int64_t)(ka + j_first) * p.sv_t;
+  auto copy_k = [&](KA_LDS char* dst) {
+    const int rows = min(lk - ck_j0, BN);
 #pragma unroll
     for (int r = 0; r < INSTS; ++r)
-      dma_16b(t_k, rows * (int)p.sk_t * 2, kv + (wave * INSTS + r) * 1024, v_block(kv_off, p.sk_t, r));
-    t_j0 += BN;
-    t_k += k_step;
+      dma_16b(c_k, rows * (int)p.sk_t * 2, dst + (wave * INSTS + r) * 1024, s_block(k_off, r));
+    ck_j0 += BN;
+    c_k += k_step;
   };
-  const int k_read = k_offset<D>(key_row(col), half) + dh * QC * 512;  // this wave's chunks of the key rows
-  const int g = lane >> 4, jl = lane & 15;
-  const int v_read = v_offset<D>(8 * (g >> 1) + (jl >> 2), 16 * (g & 1) + 4 * (jl & 3)) + dh * OB * 256;
+  auto copy_v = [&]() {
+    const int rows = min(lk - cv_j0, BN);
+#pragma unroll
+    for (int r = 0; r < INSTS; ++r)
+      dma_16b(c_v, rows * (int)p.sv_t * 2, vt + (wave * INSTS + r) * 1024, s_block(v_off, r));
+    cv_j0 += BN;
+    c_v += v_step;
+  };
+  // row reads of this wave's chunk dh*32 + 2 dc + half: k_read[dc & 1] + (dc >> 1) * 1024; transposed reads of its
+  // columns dh*256 + db*32 ..: t_read[rr] + kc * (D/8) * 256 + (dh * 8 + db) * 1024
+  const int k_read[2] = {s_offset<D>(key_row(col), half) + dh * 8192,
+                         s_offset<D>(key_row(col), 2 + half) + dh * 8192};
+  const int t_read[2] = {s_tr_base(lane, 0) + dh * 8192, s_tr_base(lane, 1) + dh * 8192};
   f32x16 acc[OB];
 #pragma unroll
   for (int db = 0; db < OB; ++db) acc[db] = f32x16{};
@@ -192,29 +186,30 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void bwd_dq_pair_kernel(BwdPara
   const KA_LDS f32x4* const other = (const KA_LDS f32x4*)&xch[wave ^ 1][0];
 
   if (n_steps > 0) {
-    copy_rows();
-    copy_trans();
+    copy_k(k0);
+    copy_v();
   }
   wait_vmcnt<0>();
   __syncthreads();
   int j0 = j_first;
-  for (int s = 0; s < n_steps; ++s) {
+  auto step = [&](int s, const KA_LDS char* kt, KA_LDS char* kn) {
     const bool act = j0 < b.whi && j0 + BN > b.wlo;  // both waves of a pair decide alike (same vectors)
     const bool ahead = s + 1 < n_steps;
+    if (ahead) copy_k(kn);  // its buffer was last read before the previous step's second barrier
     f32x16 st = f32x16{}, dpt = f32x16{};
     if (act) {  // partial S^T = K Q^T and dP^T = V dO^T over this wave's half of D
 #pragma unroll
       for (int dc = 0; dc < QC; ++dc) {
-        const bf16x8 a = *(const KA_LDS bf16x8*)(kk + k_read + dc * 512);
+        const int at = k_read[dc & 1] + (dc >> 1) * 1024;
+        const bf16x8 a = *(const KA_LDS bf16x8*)(kt + at);
         st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qop[dc], st, 0, 0, 0);
-        const bf16x8 v = *(const KA_LDS bf16x8*)(vk + k_read + dc * 512);
+        const bf16x8 v = *(const KA_LDS bf16x8*)(vt + at);
         dpt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v, dop[dc], dpt, 0, 0, 0);
       }
       exchange_write(mine, lane, st, dpt, true);
     }
-    __syncthreads();  // 1: the step's row tiles are read and the partials written
-    if (ahead) copy_rows();
-    bf16x8 dsb[KC];
+    __syncthreads();  // 1: V is read and the partials written
+    if (ahead) copy_v();
     if (act) {
       exchange_add(other, lane, dh, st, dpt, true);
       float x[KC][8];
@@ -233,36 +228,36 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void bwd_dq_pair_kernel(BwdPara
             x[kc][t] = vis ? x[kc][t] : -INFINITY;
           }
       }
+      bf16x8 dsb[KC];
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc)
 #pragma unroll
         for (int t = 0; t < 8; ++t)
           dsb[kc][t] = (__bf16)(__builtin_amdgcn_exp2f(x[kc][t]) * (dpt[kc * 8 + t] - dsum));
-    }
-    // the transposed tile of this step (copied at the end of the last step) has landed; the next step's row tiles
-    // (just issued) may still be in flight
-    if (ahead) wait_vmcnt<2 * INSTS>(); else wait_vmcnt<0>();
-    __syncthreads();  // 2: every wave's part of the transposed tile is in LDS; the partners' partials are read
-    if (act) {  // dQ^T (this wave's half of D) += K^T dS^T, K read transposed
+      // dQ^T (this wave's half of D) += K^T dS^T, K read transposed
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc)
 #pragma unroll
         for (int db = 0; db < OB; ++db) {
-          bf16x4 kt[2];
+          bf16x4 kx[2];
 #pragma unroll
           for (int rr = 0; rr < 2; ++rr)
-            kt[rr] = __builtin_bit_cast(
-                bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                            (KA_LDS s16x4*)(kv + v_read + (kc * 4 + rr) * (D / 16) * 128 + db * 256)));
-          const bf16x8 a = __builtin_shufflevector(kt[0], kt[1], 0, 1, 2, 3, 4, 5, 6, 7);
+            kx[rr] = __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                                    (KA_LDS s16x4*)(kt + t_read[rr] + kc * (D / 8) * 256 + db * 1024)));
+          const bf16x8 a = __builtin_shufflevector(kx[0], kx[1], 0, 1, 2, 3, 4, 5, 6, 7);
           acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, dsb[kc], acc[db], 0, 0, 0);
         }
     }
-    wait_vmcnt<0>();  // the next step's row tiles
-    __syncthreads();  // 3: the transposed tile is read; the next row tiles are in LDS
-    if (ahead) copy_trans();
+    wait_vmcnt<0>();  // the next step's K and V
+    __syncthreads();  // 2: they are in LDS; this step's K and the partners' partials are read
     j0 += BN;
+  };
+  int s = 0;
+  for (; s + 1 < n_steps; s += 2) {
+    step(s, k0, k1);
+    step(s + 1, k1, k0);
   }
+  if (s < n_steps) step(s, k0, k1);
 
   if (valid) {  // lane (col, half) holds d = dh*DH + db*32 + (j/4)*8 + half*4 + j%4
     uint16_t* dp = p.dq + (int64_t)(qa + pos) * p.sdq_t + (int64_t)head * p.sdq_h + dh * DH + half * 4;
@@ -288,12 +283,13 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void bwd_dkdv_pair_kernel(BwdPa
   constexpr int DH = D / 2, QC = DH / 16, OB = DH / 32, KC = BQ / 16;
   constexpr int TILE = BQ * D * 2, INSTS = TILE / 1024 / W;
   static_assert(INSTS * W * 1024 == TILE, "every wave copies the same number of 1 KiB blocks per tile");
-  constexpr int ROWS = INSTS * (DK ? 2 : 1);  // this wave's row-tile copies per step (the last wave adds the stats)
-  __shared__ __attribute__((aligned(1024))) char qk_s[TILE];              // Q, row-operand layout
-  __shared__ __attribute__((aligned(1024))) char ot_s[DK ? TILE : 1024];  // dO, row-operand layout (dK)
-  __shared__ __attribute__((aligned(1024))) char tr_s[TILE];  // Q (dK) or dO (dV), transposed-read layout
+  __shared__ __attribute__((aligned(1024))) char q0_s[TILE];  // Q of even steps (S layout: rows; transposed for dK)
+  __shared__ __attribute__((aligned(1024))) char q1_s[TILE];  // Q of odd steps
+  // dO: dK reads it as rows (S layout, one buffer); dV transposed (transposed-read layout, even and odd steps)
+  __shared__ __attribute__((aligned(1024))) char o0_s[TILE];
+  __shared__ __attribute__((aligned(1024))) char o1_s[DV ? TILE : 16];
   __shared__ __attribute__((aligned(256))) float st_s[2][2 * BQ];  // log2 LSE, then D, of a step's rows (by parity)
-  __shared__ __attribute__((aligned(16))) f32x4 xch[W][8 * 64];
+  __shared__ __attribute__((aligned(16))) f32x4 xch[W][(DK ? 8 : 4) * 64];
   __shared__ int red[2][W];
 
   if (p.plan[2] != BQ || p.plan[5] != W) return;
@@ -347,76 +343,67 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void bwd_dkdv_pair_kernel(BwdPa
   const int n_steps = n_rsteps * p.group;
 
   static_assert(D == 512 && INSTS == 8, "the block offsets below are those of head size 512");
-  const uint32_t qk_off = k_block_base(wave, lane, p.sq_t), ok_off = k_block_base(wave, lane, p.sdo_t);
-  const uint32_t tr_off = v_block_base(wave, lane, DK ? p.sq_t : p.sdo_t);
-  KA_LDS char* const qk = (KA_LDS char*)qk_s;
-  KA_LDS char* const ok = (KA_LDS char*)ot_s;
-  KA_LDS char* const tr = (KA_LDS char*)tr_s;
+  const uint32_t q_off = s_block_base(wave, lane, p.sq_t);
+  const uint32_t o_off = DK ? s_block_base(wave, lane, p.sdo_t) : v_block_base(wave, lane, p.sdo_t);
+  KA_LDS char* const q0 = (KA_LDS char*)q0_s;
+  KA_LDS char* const q1 = (KA_LDS char*)q1_s;
+  KA_LDS char* const o0 = (KA_LDS char*)o0_s;
+  KA_LDS char* const o1 = (KA_LDS char*)o1_s;
   KA_LDS float* const st0 = (KA_LDS float*)&st_s[0][0];
-  // cursors over (head, row step), rows from the last step down, then the group's next head (pointer increments)
+  KA_LDS float* const st1 = (KA_LDS float*)&st_s[1][0];
+  // copy cursor over (head, row step), rows from the last step down, then the group's next head (pointer increments);
+  // dK's dO copy (after a step's first barrier) takes the step the cursor last passed from o_src / o_rows
   const int r_last = r_first + (n_rsteps - 1) * BQ;
   const int h0 = kvh * p.group;
   const int64_t q_step = (int64_t)BQ * p.sq_t, o_step = (int64_t)BQ * p.sdo_t;
   const int64_t q_wrap = p.sq_h + n_rsteps * q_step, o_wrap = p.sdo_h + n_rsteps * o_step;
   const int64_t st_wrap = 2 * p.total_q + (int64_t)n_rsteps * BQ;
   const uint32_t st_off = (uint32_t)((lane >> 5) * p.total_q + (lane & 31)) * 4u;
-  const uint16_t* q0 = p.q + (int64_t)(qa + r_last) * p.sq_t + (int64_t)h0 * p.sq_h;
-  const uint16_t* o0 = p.dout + (int64_t)(qa + r_last) * p.sdo_t + (int64_t)h0 * p.sdo_h;
-  int r_r0 = r_last, r_par = 0, t_r0 = r_last;
-  const uint16_t* r_q = q0;
-  const uint16_t* r_o = o0;
-  const float* r_st = p.stats + (int64_t)h0 * 2 * p.total_q + qa + r_last;
-  const uint16_t* t_x = DK ? q0 : o0;  // the transposed tile's source (Q for dK, dO for dV)
-  const int64_t t_step = DK ? q_step : o_step, t_wrap = DK ? q_wrap : o_wrap;
-  const int64_t t_stride = DK ? p.sq_t : p.sdo_t;
-  auto copy_rows = [&]() {  // Q rows (dO rows for dK) and the rows' statistics (into the step parity's slot)
-    const int rows = min(lq - r_r0, BQ);
+  int c_r0 = r_last;
+  const uint16_t* c_q = p.q + (int64_t)(qa + r_last) * p.sq_t + (int64_t)h0 * p.sq_h;
+  const uint16_t* c_o = p.dout + (int64_t)(qa + r_last) * p.sdo_t + (int64_t)h0 * p.sdo_h;
+  const float* c_st = p.stats + (int64_t)h0 * 2 * p.total_q + qa + r_last;
+  const uint16_t* o_src = c_o;
+  int o_rows = 0;
+  // Q (and dO for dV) of the cursor's step, and its rows' statistics; the cursor moves on
+  auto copy_q = [&](KA_LDS char* dq_, KA_LDS char* do_, KA_LDS float* dst) {
+    const int rows = min(lq - c_r0, BQ);
 #pragma unroll
     for (int r = 0; r < INSTS; ++r) {
       const int at = (wave * INSTS + r) * 1024;
-      dma_16b(r_q, rows * (int)p.sq_t * 2, qk + at, k_block(qk_off, r));
-      if constexpr (DK) dma_16b(r_o, rows * (int)p.sdo_t * 2, ok + at, k_block(ok_off, r));
+      dma_16b(c_q, rows * (int)p.sq_t * 2, dq_ + at, s_block(q_off, r));
+      if constexpr (DV) dma_16b(c_o, rows * (int)p.sdo_t * 2, do_ + at, v_block(o_off, p.sdo_t, r));
     }
     if (wave == W - 1) {  // 32 log2 LSE (lanes 0-31) then 32 D (lanes 32-63), 4 B per lane; zeros past the stats
       const __amdgpu_buffer_rsrc_t rs =
-          __builtin_amdgcn_make_buffer_rsrc((void*)r_st, (short)0, (int)(p.total_q + rows) * 4, kBufferFlags);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (KA_LDS void*)(st0 + r_par * 2 * BQ), 4, st_off, 0, 0, 0);
+          __builtin_amdgcn_make_buffer_rsrc((void*)c_st, (short)0, (int)(p.total_q + rows) * 4, kBufferFlags);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (KA_LDS void*)dst, 4, st_off, 0, 0, 0);
     }
-    r_r0 -= BQ;
-    r_q -= q_step;
-    r_o -= o_step;
-    r_st -= BQ;
-    if (r_r0 < r_first) {
-      r_r0 = r_last;
-      r_q += q_wrap;
-      r_o += o_wrap;
-      r_st += st_wrap;
+    o_src = c_o;
+    o_rows = rows;
+    c_r0 -= BQ;
+    c_q -= q_step;
+    c_o -= o_step;
+    c_st -= BQ;
+    if (c_r0 < r_first) {
+      c_r0 = r_last;
+      c_q += q_wrap;
+      c_o += o_wrap;
+      c_st += st_wrap;
     }
-    r_par ^= 1;
   };
-  auto copy_trans = [&]() {
-    const int rows = min(lq - t_r0, BQ);
+  auto copy_o = [&]() {  // dK: dO rows of the step copy_q last took
 #pragma unroll
     for (int r = 0; r < INSTS; ++r)
-      dma_16b(t_x, rows * (int)t_stride * 2, tr + (wave * INSTS + r) * 1024, v_block(tr_off, t_stride, r));
-    t_r0 -= BQ;
-    t_x -= t_step;
-    if (t_r0 < r_first) {
-      t_r0 = r_last;
-      t_x += t_wrap;
-    }
+      dma_16b(o_src, o_rows * (int)p.sdo_t * 2, o0 + (wave * INSTS + r) * 1024, s_block(o_off, r));
   };
-  auto wait_rows = [&](bool ahead) {  // at most the row copies just issued outstanding
-    if (!ahead) {
-      wait_vmcnt<0>();
-    } else if (wave == W - 1) {
-      wait_vmcnt<ROWS + 1>();
-    } else {
-      wait_vmcnt<ROWS>();
-    }
-  };
-  const int q_read = k_offset<D>(key_row(col), half) + dh * QC * 512;
+  // row reads of this wave's chunk dh*32 + 2 dc + half: q_read[dc & 1] + (dc >> 1) * 1024; transposed reads of its
+  // columns dh*256 + db*32 ..: t_read[rr] + kc * (D/8) * 256 + (dh * 8 + db) * 1024 (S layout, dK) or
+  // v_read + (kc * 4 + rr) * (D/16) * 128 + db * 256 (transposed-read layout, dV)
+  const int q_read[2] = {s_offset<D>(key_row(col), half) + dh * 8192,
+                         s_offset<D>(key_row(col), 2 + half) + dh * 8192};
   const int g = lane >> 4, jl = lane & 15;
+  const int t_read[2] = {s_tr_base(lane, 0) + dh * 8192, s_tr_base(lane, 1) + dh * 8192};
   const int v_read = v_offset<D>(8 * (g >> 1) + (jl >> 2), 16 * (g & 1) + 4 * (jl & 3)) + dh * OB * 256;
   f32x16 acc[OB];  // dK^T or dV^T, this wave's half of D
 #pragma unroll
@@ -426,35 +413,37 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void bwd_dkdv_pair_kernel(BwdPa
   const KA_LDS f32x4* const other = (const KA_LDS f32x4*)&xch[wave ^ 1][0];
 
   if (n_steps > 0) {
-    copy_rows();
-    copy_trans();
+    copy_q(q0, o0, st0);
+    if constexpr (DK) copy_o();
   }
   wait_vmcnt<0>();
   __syncthreads();
-  int r0 = r_last, par = 0;
-  for (int s = 0; s < n_steps; ++s) {
+  int r0 = r_last;
+  auto step = [&](int s, const KA_LDS char* qt, const KA_LDS char* ot, const KA_LDS float* tst, KA_LDS char* qn,
+                  KA_LDS char* on, KA_LDS float* sn) {
     const bool act = r0 < b.whi && r0 + BQ > b.wlo;
     const bool ahead = s + 1 < n_steps;
+    if (ahead) copy_q(qn, on, sn);  // their buffers were last read before the previous step's second barrier
     f32x16 st = f32x16{}, dpt = f32x16{};
     if (act) {  // partial S = Q K^T (and dP = dO V^T) over this wave's half of D
 #pragma unroll
       for (int dc = 0; dc < QC; ++dc) {
-        const bf16x8 a = *(const KA_LDS bf16x8*)(qk + q_read + dc * 512);
+        const int at = q_read[dc & 1] + (dc >> 1) * 1024;
+        const bf16x8 a = *(const KA_LDS bf16x8*)(qt + at);
         st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, kop[dc], st, 0, 0, 0);
         if constexpr (DK) {
-          const bf16x8 o = *(const KA_LDS bf16x8*)(ok + q_read + dc * 512);
+          const bf16x8 o = *(const KA_LDS bf16x8*)(o0 + at);
           dpt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(o, vop[dc], dpt, 0, 0, 0);
         }
       }
       exchange_write(mine, lane, st, dpt, DK);
     }
-    __syncthreads();  // 1: the row tiles are read and the partials written
-    if (ahead) copy_rows();  // the statistics go to the other parity's slot: this step's stay readable
-    bf16x8 pb[KC];
+    __syncthreads();  // 1: dO rows (dK) are read and the partials written
+    if constexpr (DK)
+      if (ahead) copy_o();
     if (act) {
       exchange_add(other, lane, dh, st, dpt, DK);
       // the rows' statistics four at a time (registers u = jj / 4 hold rows (u/2)*16 + half*8 + (u%2)*4 ..)
-      const KA_LDS float* tst = st0 + par * 2 * BQ;
       float x[2 * KC * 4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
@@ -471,6 +460,7 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void bwd_dkdv_pair_kernel(BwdPa
           x[jj] = vis ? x[jj] : -INFINITY;
         }
       }
+      bf16x8 pb[KC];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {  // P (dV) or dS (dK), four registers at a time
         f32x4 ds = {};
@@ -482,30 +472,32 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void bwd_dkdv_pair_kernel(BwdPa
           pb[jj >> 3][jj & 7] = DK ? (__bf16)(pr * (dpt[jj] - ds[e])) : (__bf16)pr;
         }
       }
-    }
-    wait_rows(ahead);  // this step's transposed tile has landed
-    __syncthreads();   // 2: every wave's part of it is in LDS; the partners' partials are read
-    if (act) {  // dV^T += dO^T P or dK^T += Q^T dS, this wave's half of D, the operand read transposed
+      // dV^T += dO^T P or dK^T += Q^T dS, this wave's half of D, the operand read transposed
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc)
 #pragma unroll
         for (int db = 0; db < OB; ++db) {
           bf16x4 xt[2];
 #pragma unroll
-          for (int rr = 0; rr < 2; ++rr)
-            xt[rr] = __builtin_bit_cast(
-                bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                            (KA_LDS s16x4*)(tr + v_read + (kc * 4 + rr) * (D / 16) * 128 + db * 256)));
+          for (int rr = 0; rr < 2; ++rr) {
+            const KA_LDS char* at = DK ? qt + t_read[rr] + kc * (D / 8) * 256 + db * 1024
+                                       : ot + v_read + (kc * 4 + rr) * (D / 16) * 128 + db * 256;
+            xt[rr] = __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((KA_LDS s16x4*)at));
+          }
           const bf16x8 a = __builtin_shufflevector(xt[0], xt[1], 0, 1, 2, 3, 4, 5, 6, 7);
           acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[kc], acc[db], 0, 0, 0);
         }
     }
-    wait_vmcnt<0>();
-    __syncthreads();  // 3: the transposed tile is read; the next row tiles and statistics are in LDS
-    if (ahead) copy_trans();
+    wait_vmcnt<0>();  // the next step's tiles and statistics
+    __syncthreads();  // 2: they are in LDS; this step's tiles and the partners' partials are read
     r0 = r0 == r_first ? r_last : r0 - BQ;
-    par ^= 1;
+  };
+  int s = 0;
+  for (; s + 1 < n_steps; s += 2) {
+    step(s, q0, o0, st0, q1, o1, st1);
+    step(s + 1, q1, o1, st1, q0, o0, st0);
   }
+  if (s < n_steps) step(s, q0, o0, st0, q1, o1, st1);
 
   if (valid) {  // lane (col, half) holds d = dh*DH + db*32 + (j/4)*8 + half*4 + j%4 of its key
     uint16_t* gp = DK ? p.dk + (int64_t)(ka + key) * p.sdk_t + (int64_t)kvh * p.sdk_h
