@@ -273,23 +273,26 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void bwd_dq_pair_kernel(BwdPara
   }
 }
 
-// ---- dK (MODE 2) or dV (MODE 1): key tiles of two pairs (64 keys), 32 query rows of one head per step, each head of
-// the GQA group in turn, rows from the last step down (as attn_bwd.hip's key-stationary kernel)
-template <int D, int MODE>
+// ---- dK and dV: key tiles of two pairs (64 keys), 32 query rows of one head per step, each head of the GQA group in
+// turn, rows from the last step down (as attn_bwd.hip's key-stationary kernel). A wave holds half of D of both
+// accumulators (2 x 128 registers) and of K and V. The pair splits a step's softmax by row block: wave dh computes P
+// and dS of rows dh*16 .. +16 from the partner's partial S and dP of those rows (low half + high half), and the two
+// swap their P and dS (bf16, the MFMA operands) through LDS: 24 KiB of exchange instead of 32, so Q and dO (read as
+// rows and transposed) both get two buffers.
+template <int D>
 __global__ __launch_bounds__(64 * kPairWaves, 1) void bwd_dkdv_pair_kernel(BwdParams p) {
-  static_assert(MODE == 1 || MODE == 2, "dV or dK");
-  constexpr bool DV = MODE == 1, DK = MODE == 2;
   constexpr int W = kPairWaves, BQ = kPairStep;
   constexpr int DH = D / 2, QC = DH / 16, OB = DH / 32, KC = BQ / 16;
+  static_assert(KC == 2, "the waves of a pair take one 16-row block of a step each");
   constexpr int TILE = BQ * D * 2, INSTS = TILE / 1024 / W;
   static_assert(INSTS * W * 1024 == TILE, "every wave copies the same number of 1 KiB blocks per tile");
-  __shared__ __attribute__((aligned(1024))) char q0_s[TILE];  // Q of even steps (S layout: rows; transposed for dK)
+  __shared__ __attribute__((aligned(1024))) char q0_s[TILE];  // Q of even steps (S layout: rows for S, transposed for dK)
   __shared__ __attribute__((aligned(1024))) char q1_s[TILE];  // Q of odd steps
-  // dO: dK reads it as rows (S layout, one buffer); dV transposed (transposed-read layout, even and odd steps)
-  __shared__ __attribute__((aligned(1024))) char o0_s[TILE];
-  __shared__ __attribute__((aligned(1024))) char o1_s[DV ? TILE : 16];
+  __shared__ __attribute__((aligned(1024))) char o0_s[TILE];  // dO of even steps (S layout: rows for dP, transposed for dV)
+  __shared__ __attribute__((aligned(1024))) char o1_s[TILE];  // dO of odd steps
   __shared__ __attribute__((aligned(256))) float st_s[2][2 * BQ];  // log2 LSE, then D, of a step's rows (by parity)
-  __shared__ __attribute__((aligned(16))) f32x4 xch[W][(DK ? 8 : 4) * 64];
+  __shared__ __attribute__((aligned(16))) f32x4 xch[W][4 * 64];    // partial S and dP of the partner's row block
+  __shared__ __attribute__((aligned(16))) bf16x8 pxch[W][2 * 64];  // P and dS of the wave's row block
   __shared__ int red[2][W];
 
   if (p.plan[2] != BQ || p.plan[5] != W) return;
@@ -313,7 +316,7 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void bwd_dkdv_pair_kernel(BwdPa
     red[0][wave] = b.wlo;
     red[1][wave] = b.whi;
   }
-  // this wave's half of K (and of V for dK) of the lane's key as B operands
+  // this wave's half of K and V of the lane's key as B operands
   bf16x8 kop[QC], vop[QC];
   {
     const uint16_t* kp = p.k + (int64_t)(ka + key) * p.sk_t + (int64_t)kvh * p.sk_h + dh * DH + half * 8;
@@ -323,10 +326,10 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void bwd_dkdv_pair_kernel(BwdPa
       u32x4 x = {0, 0, 0, 0}, y = {0, 0, 0, 0};
       if (valid) {
         x = *(const u32x4*)(kp + dc * 16);
-        if constexpr (DK) y = *(const u32x4*)(vp + dc * 16);
+        y = *(const u32x4*)(vp + dc * 16);
       }
       kop[dc] = __builtin_bit_cast(bf16x8, x);
-      if constexpr (DK) vop[dc] = __builtin_bit_cast(bf16x8, y);
+      vop[dc] = __builtin_bit_cast(bf16x8, y);
     }
   }
   __syncthreads();
@@ -343,16 +346,14 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void bwd_dkdv_pair_kernel(BwdPa
   const int n_steps = n_rsteps * p.group;
 
   static_assert(D == 512 && INSTS == 8, "the block offsets below are those of head size 512");
-  const uint32_t q_off = s_block_base(wave, lane, p.sq_t);
-  const uint32_t o_off = DK ? s_block_base(wave, lane, p.sdo_t) : v_block_base(wave, lane, p.sdo_t);
+  const uint32_t q_off = s_block_base(wave, lane, p.sq_t), o_off = s_block_base(wave, lane, p.sdo_t);
   KA_LDS char* const q0 = (KA_LDS char*)q0_s;
   KA_LDS char* const q1 = (KA_LDS char*)q1_s;
   KA_LDS char* const o0 = (KA_LDS char*)o0_s;
   KA_LDS char* const o1 = (KA_LDS char*)o1_s;
   KA_LDS float* const st0 = (KA_LDS float*)&st_s[0][0];
   KA_LDS float* const st1 = (KA_LDS float*)&st_s[1][0];
-  // copy cursor over (head, row step), rows from the last step down, then the group's next head (pointer increments);
-  // dK's dO copy (after a step's first barrier) takes the step the cursor last passed from o_src / o_rows
+  // copy cursor over (head, row step), rows from the last step down, then the group's next head (pointer increments)
   const int r_last = r_first + (n_rsteps - 1) * BQ;
   const int h0 = kvh * p.group;
   const int64_t q_step = (int64_t)BQ * p.sq_t, o_step = (int64_t)BQ * p.sdo_t;
@@ -363,24 +364,20 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void bwd_dkdv_pair_kernel(BwdPa
   const uint16_t* c_q = p.q + (int64_t)(qa + r_last) * p.sq_t + (int64_t)h0 * p.sq_h;
   const uint16_t* c_o = p.dout + (int64_t)(qa + r_last) * p.sdo_t + (int64_t)h0 * p.sdo_h;
   const float* c_st = p.stats + (int64_t)h0 * 2 * p.total_q + qa + r_last;
-  const uint16_t* o_src = c_o;
-  int o_rows = 0;
-  // Q (and dO for dV) of the cursor's step, and its rows' statistics; the cursor moves on
-  auto copy_q = [&](KA_LDS char* dq_, KA_LDS char* do_, KA_LDS float* dst) {
+  // Q, dO and the rows' statistics of the cursor's step; the cursor moves on
+  auto copy_step = [&](KA_LDS char* dq_, KA_LDS char* do_, KA_LDS float* dst) {
     const int rows = min(lq - c_r0, BQ);
 #pragma unroll
     for (int r = 0; r < INSTS; ++r) {
       const int at = (wave * INSTS + r) * 1024;
       dma_16b(c_q, rows * (int)p.sq_t * 2, dq_ + at, s_block(q_off, r));
-      if constexpr (DV) dma_16b(c_o, rows * (int)p.sdo_t * 2, do_ + at, v_block(o_off, p.sdo_t, r));
+      dma_16b(c_o, rows * (int)p.sdo_t * 2, do_ + at, s_block(o_off, r));
     }
     if (wave == W - 1) {  // 32 log2 LSE (lanes 0-31) then 32 D (lanes 32-63), 4 B per lane; zeros past the stats
       const __amdgpu_buffer_rsrc_t rs =
           __builtin_amdgcn_make_buffer_rsrc((void*)c_st, (short)0, (int)(p.total_q + rows) * 4, kBufferFlags);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (KA_LDS void*)dst, 4, st_off, 0, 0, 0);
     }
-    o_src = c_o;
-    o_rows = rows;
     c_r0 -= BQ;
     c_q -= q_step;
     c_o -= o_step;
@@ -392,104 +389,127 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void bwd_dkdv_pair_kernel(BwdPa
       c_st += st_wrap;
     }
   };
-  auto copy_o = [&]() {  // dK: dO rows of the step copy_q last took
-#pragma unroll
-    for (int r = 0; r < INSTS; ++r)
-      dma_16b(o_src, o_rows * (int)p.sdo_t * 2, o0 + (wave * INSTS + r) * 1024, s_block(o_off, r));
-  };
-  // row reads of this wave's chunk dh*32 + 2 dc + half: q_read[dc & 1] + (dc >> 1) * 1024; transposed reads of its
-  // columns dh*256 + db*32 ..: t_read[rr] + kc * (D/8) * 256 + (dh * 8 + db) * 1024 (S layout, dK) or
-  // v_read + (kc * 4 + rr) * (D/16) * 128 + db * 256 (transposed-read layout, dV)
-  const int q_read[2] = {s_offset<D>(key_row(col), half) + dh * 8192,
-                         s_offset<D>(key_row(col), 2 + half) + dh * 8192};
-  const int g = lane >> 4, jl = lane & 15;
+  // row reads of this wave's chunk dh*32 + 2 dc + half: row_read[dc & 1] + (dc >> 1) * 1024; transposed reads of its
+  // columns dh*256 + db*32 ..: t_read[rr] + kc * (D/8) * 256 + db * 1024
+  const int row_read[2] = {s_offset<D>(key_row(col), half) + dh * 8192,
+                           s_offset<D>(key_row(col), 2 + half) + dh * 8192};
   const int t_read[2] = {s_tr_base(lane, 0) + dh * 8192, s_tr_base(lane, 1) + dh * 8192};
-  const int v_read = v_offset<D>(8 * (g >> 1) + (jl >> 2), 16 * (g & 1) + 4 * (jl & 3)) + dh * OB * 256;
-  f32x16 acc[OB];  // dK^T or dV^T, this wave's half of D
+  f32x16 dk[OB], dv[OB];  // dK^T and dV^T, this wave's half of D
 #pragma unroll
-  for (int db = 0; db < OB; ++db) acc[db] = f32x16{};
+  for (int db = 0; db < OB; ++db) {
+    dk[db] = f32x16{};
+    dv[db] = f32x16{};
+  }
   const float c = p.c;
   KA_LDS f32x4* const mine = (KA_LDS f32x4*)&xch[wave][0];
   const KA_LDS f32x4* const other = (const KA_LDS f32x4*)&xch[wave ^ 1][0];
+  KA_LDS bf16x8* const pmine = (KA_LDS bf16x8*)&pxch[wave][0];
+  const KA_LDS bf16x8* const pother = (const KA_LDS bf16x8*)&pxch[wave ^ 1][0];
 
-  if (n_steps > 0) {
-    copy_q(q0, o0, st0);
-    if constexpr (DK) copy_o();
-  }
+  if (n_steps > 0) copy_step(q0, o0, st0);
   wait_vmcnt<0>();
   __syncthreads();
   int r0 = r_last;
   auto step = [&](int s, const KA_LDS char* qt, const KA_LDS char* ot, const KA_LDS float* tst, KA_LDS char* qn,
                   KA_LDS char* on, KA_LDS float* sn) {
-    const bool act = r0 < b.whi && r0 + BQ > b.wlo;
-    const bool ahead = s + 1 < n_steps;
-    if (ahead) copy_q(qn, on, sn);  // their buffers were last read before the previous step's second barrier
+    const bool act = r0 < b.whi && r0 + BQ > b.wlo;  // both waves of a pair decide alike (same keys)
+    if (s + 1 < n_steps) copy_step(qn, on, sn);  // their buffers were last read before the previous step's end
     f32x16 st = f32x16{}, dpt = f32x16{};
-    if (act) {  // partial S = Q K^T (and dP = dO V^T) over this wave's half of D
+    if (act) {  // partial S = Q K^T and dP = dO V^T over this wave's half of D
 #pragma unroll
       for (int dc = 0; dc < QC; ++dc) {
-        const int at = q_read[dc & 1] + (dc >> 1) * 1024;
+        const int at = row_read[dc & 1] + (dc >> 1) * 1024;
         const bf16x8 a = *(const KA_LDS bf16x8*)(qt + at);
         st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, kop[dc], st, 0, 0, 0);
-        if constexpr (DK) {
-          const bf16x8 o = *(const KA_LDS bf16x8*)(o0 + at);
-          dpt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(o, vop[dc], dpt, 0, 0, 0);
-        }
+        const bf16x8 o = *(const KA_LDS bf16x8*)(ot + at);
+        dpt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(o, vop[dc], dpt, 0, 0, 0);
       }
-      exchange_write(mine, lane, st, dpt, DK);
+      // registers 8 kc .. 8 kc + 7 hold rows kc*16 + half*8 .. +8: the partner's block (kc = 1 - dh) to it
+      f32x4 w0, w1, w2, w3;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        w0[e] = dh ? st[e] : st[8 + e];
+        w1[e] = dh ? st[4 + e] : st[12 + e];
+        w2[e] = dh ? dpt[e] : dpt[8 + e];
+        w3[e] = dh ? dpt[4 + e] : dpt[12 + e];
+      }
+      mine[lane] = w0;
+      mine[64 + lane] = w1;
+      mine[128 + lane] = w2;
+      mine[192 + lane] = w3;
     }
-    __syncthreads();  // 1: dO rows (dK) are read and the partials written
-    if constexpr (DK)
-      if (ahead) copy_o();
-    if (act) {
-      exchange_add(other, lane, dh, st, dpt, DK);
-      // the rows' statistics four at a time (registers u = jj / 4 hold rows (u/2)*16 + half*8 + (u%2)*4 ..)
-      float x[2 * KC * 4];
+    __syncthreads();  // 1: the partials are written
+    bf16x8 pm, dm;
+    if (act) {  // this wave's block: S and dP summed low half + high half, P and dS of rows r0 + dh*16 + half*8 + t
+      const f32x4 x0 = other[lane], x1 = other[64 + lane], x2 = other[128 + lane], x3 = other[192 + lane];
+      float sv[8], pv[8];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const f32x4 ls = *(const KA_LDS f32x4*)(tst + (u >> 1) * 16 + half * 8 + (u & 1) * 4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) x[4 * u + e] = __builtin_fmaf(st[4 * u + e], c, -ls[e]);
+      for (int e = 0; e < 4; ++e) {
+        const float s0 = dh ? st[8 + e] : st[e], s1 = dh ? st[12 + e] : st[4 + e];
+        const float p0 = dh ? dpt[8 + e] : dpt[e], p1 = dh ? dpt[12 + e] : dpt[4 + e];
+        sv[e] = dh ? x0[e] + s0 : s0 + x0[e];
+        sv[4 + e] = dh ? x1[e] + s1 : s1 + x1[e];
+        pv[e] = dh ? x2[e] + p0 : p0 + x2[e];
+        pv[4 + e] = dh ? x3[e] + p1 : p1 + x3[e];
       }
-      if (!(r0 >= b.wflo && r0 + BQ <= b.wfhi)) {
+      const KA_LDS float* rs = tst + dh * 16 + half * 8;
+      const f32x4 l0 = *(const KA_LDS f32x4*)rs, l1 = *(const KA_LDS f32x4*)(rs + 4);
+      const f32x4 d0 = *(const KA_LDS f32x4*)(rs + BQ), d1 = *(const KA_LDS f32x4*)(rs + BQ + 4);
+      float x[8];
 #pragma unroll
-        for (int jj = 0; jj < 2 * KC * 4; ++jj) {
-          const int row = r0 + (jj >> 3) * 16 + half * 8 + (jj & 7);
+      for (int e = 0; e < 4; ++e) {
+        x[e] = __builtin_fmaf(sv[e], c, -l0[e]);
+        x[4 + e] = __builtin_fmaf(sv[4 + e], c, -l1[e]);
+      }
+      if (!(r0 >= b.wflo && r0 + BQ <= b.wfhi)) {  // one uniform branch around the masking
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          const int row = r0 + dh * 16 + half * 8 + t;
           const bool vis = ((unsigned)(row - b.lo) < (unsigned)(b.hi - b.lo)) |
                            ((unsigned)(row - b.sl) < (unsigned)(b.sh - b.sl));
-          x[jj] = vis ? x[jj] : -INFINITY;
+          x[t] = vis ? x[t] : -INFINITY;
         }
       }
-      bf16x8 pb[KC];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {  // P (dV) or dS (dK), four registers at a time
-        f32x4 ds = {};
-        if constexpr (DK) ds = *(const KA_LDS f32x4*)(tst + BQ + (u >> 1) * 16 + half * 8 + (u & 1) * 4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int jj = 4 * u + e;
-          const float pr = __builtin_amdgcn_exp2f(x[jj]);
-          pb[jj >> 3][jj & 7] = DK ? (__bf16)(pr * (dpt[jj] - ds[e])) : (__bf16)pr;
-        }
+      for (int t = 0; t < 8; ++t) {
+        const float pr = __builtin_amdgcn_exp2f(x[t]);
+        pm[t] = (__bf16)pr;
+        dm[t] = (__bf16)(pr * (pv[t] - (t < 4 ? d0[t] : d1[t - 4])));
       }
-      // dV^T += dO^T P or dK^T += Q^T dS, this wave's half of D, the operand read transposed
+      pmine[lane] = pm;
+      pmine[64 + lane] = dm;
+    }
+    __syncthreads();  // 2: P and dS of both blocks are written
+    if (act) {
+      const bf16x8 po = pother[lane], dso = pother[64 + lane];
+      bf16x8 pb[KC], dsb[KC];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        pb[0][t] = dh ? po[t] : pm[t];
+        pb[1][t] = dh ? pm[t] : po[t];
+        dsb[0][t] = dh ? dso[t] : dm[t];
+        dsb[1][t] = dh ? dm[t] : dso[t];
+      }
+      // dV^T += dO^T P and dK^T += Q^T dS, this wave's half of D, dO and Q read transposed
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc)
 #pragma unroll
         for (int db = 0; db < OB; ++db) {
-          bf16x4 xt[2];
+          bf16x4 ox[2], qx[2];
 #pragma unroll
           for (int rr = 0; rr < 2; ++rr) {
-            const KA_LDS char* at = DK ? qt + t_read[rr] + kc * (D / 8) * 256 + db * 1024
-                                       : ot + v_read + (kc * 4 + rr) * (D / 16) * 128 + db * 256;
-            xt[rr] = __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((KA_LDS s16x4*)at));
+            const int at = t_read[rr] + kc * (D / 8) * 256 + db * 1024;
+            ox[rr] = __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((KA_LDS s16x4*)(ot + at)));
+            qx[rr] = __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((KA_LDS s16x4*)(qt + at)));
           }
-          const bf16x8 a = __builtin_shufflevector(xt[0], xt[1], 0, 1, 2, 3, 4, 5, 6, 7);
-          acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[kc], acc[db], 0, 0, 0);
+          const bf16x8 ao = __builtin_shufflevector(ox[0], ox[1], 0, 1, 2, 3, 4, 5, 6, 7);
+          dv[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ao, pb[kc], dv[db], 0, 0, 0);
+          const bf16x8 aq = __builtin_shufflevector(qx[0], qx[1], 0, 1, 2, 3, 4, 5, 6, 7);
+          dk[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aq, dsb[kc], dk[db], 0, 0, 0);
         }
     }
     wait_vmcnt<0>();  // the next step's tiles and statistics
-    __syncthreads();  // 2: they are in LDS; this step's tiles and the partners' partials are read
+    __syncthreads();  // 3: they are in LDS; this step's tiles and the exchanges are read
     r0 = r0 == r_first ? r_last : r0 - BQ;
   };
   int s = 0;
@@ -500,18 +520,19 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void bwd_dkdv_pair_kernel(BwdPa
   if (s < n_steps) step(s, q0, o0, st0, q1, o1, st1);
 
   if (valid) {  // lane (col, half) holds d = dh*DH + db*32 + (j/4)*8 + half*4 + j%4 of its key
-    uint16_t* gp = DK ? p.dk + (int64_t)(ka + key) * p.sdk_t + (int64_t)kvh * p.sdk_h
-                      : p.dv + (int64_t)(ka + key) * p.sdv_t + (int64_t)kvh * p.sdv_h;
-    gp += dh * DH + half * 4;
-    const float f = DK ? p.scale : 1.f;
+    uint16_t* kq = p.dk + (int64_t)(ka + key) * p.sdk_t + (int64_t)kvh * p.sdk_h + dh * DH + half * 4;
+    uint16_t* vq = p.dv + (int64_t)(ka + key) * p.sdv_t + (int64_t)kvh * p.sdv_h + dh * DH + half * 4;
 #pragma unroll
     for (int db = 0; db < OB; ++db)
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
-        u32x2 w;
-        w[0] = pack_bf16(acc[db][g4 * 4] * f, acc[db][g4 * 4 + 1] * f);
-        w[1] = pack_bf16(acc[db][g4 * 4 + 2] * f, acc[db][g4 * 4 + 3] * f);
-        *(u32x2*)(gp + db * 32 + g4 * 8) = w;
+        u32x2 a, w;
+        a[0] = pack_bf16(dk[db][g4 * 4] * p.scale, dk[db][g4 * 4 + 1] * p.scale);
+        a[1] = pack_bf16(dk[db][g4 * 4 + 2] * p.scale, dk[db][g4 * 4 + 3] * p.scale);
+        *(u32x2*)(kq + db * 32 + g4 * 8) = a;
+        w[0] = pack_bf16(dv[db][g4 * 4], dv[db][g4 * 4 + 1]);
+        w[1] = pack_bf16(dv[db][g4 * 4 + 2], dv[db][g4 * 4 + 3]);
+        *(u32x2*)(vq + db * 32 + g4 * 8) = w;
       }
   }
 }
@@ -534,8 +555,7 @@ hipError_t launch_bwd_pair(const BwdParams& p, const Geometry& gq, const Geometr
   pk.n_hg = gk.n_hg;
   if (items_k > 0) {
     const dim3 grid((unsigned)(items_k * gk.n_hg));
-    hipLaunchKernelGGL((bwd_dkdv_pair_kernel<D, 1>), grid, dim3(64 * kPairWaves), 0, stream, pk);
-    hipLaunchKernelGGL((bwd_dkdv_pair_kernel<D, 2>), grid, dim3(64 * kPairWaves), 0, stream, pk);
+    hipLaunchKernelGGL(bwd_dkdv_pair_kernel<D>, grid, dim3(64 * kPairWaves), 0, stream, pk);
   }
   return hipGetLastError();
 }
