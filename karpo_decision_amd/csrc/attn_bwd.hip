@@ -10,12 +10,13 @@
 //   * bwd_stats_kernel: per (head, query row) the log2-domain LSE (+inf for a row that sees no key, so its P are 0)
 //     and D;
 //   * bwd_dq_kernel (query-stationary, the forward's tiles): Q and dO of 32 query vectors per wave as MFMA B operands
-//     in registers, K and V streamed through LDS; S^T = K Q^T and dP^T = V dO^T with K and V read as row operands
-//     (K layout), dQ^T += K^T dS^T with K read transposed (V layout), so K is staged in both layouts;
+//     in registers, K and V streamed through LDS; S^T = K Q^T and dP^T = V dO^T with K and V read as row operands,
+//     dQ^T += K^T dS^T with K read transposed from the same tile (the S layout of mfma_common.h serves both reads);
 //   * bwd_dkdv_kernel (key-stationary, tiles of 128 keys, four waves of 32): K and V of the wave's keys in registers,
 //     the query rows that see the tile streamed in steps of 32 rows of one head (every head of the GQA group in turn,
 //     which sums the group's gradients): S = Q K^T and dP = dO V^T with Q and dO as row operands, dV^T += dO^T P and
-//     dK^T += Q^T dS with Q and dO read transposed, so Q and dO are staged in both layouts. One launch computes both
+//     dK^T += Q^T dS with Q and dO read transposed from the same tiles (S layout; a dV-only launch stages dO in the
+//     transposed-read layout, whose copies read whole rows). One launch computes both
 //     (MODE 3), or two launches compute dV (MODE 1) and dK (MODE 2), each recomputing S: always at head size 256
 //     (both accumulators and both operands do not fit one wave's registers), and at 128 for packs with many key tiles
 //     (two or three waves per SIMD instead of one overlap each other's softmax and MFMA work; a small pack has too
