@@ -10,8 +10,9 @@
 // Mapping onto a CU. One work item = one query tile x one head group, over all or one part of the tile's key steps:
 //   * each wave holds 32 query vectors (position, head) of the tile in registers as MFMA B operands; the waves of a
 //     workgroup share one K/V stream (wide tiles: 12 waves at head_dim 128, three per SIMD, so one wave's softmax
-//     VALU work runs beside another wave's MFMAs; 8 at 256; 4 at 64), or a workgroup is one wave (narrow tiles for
-//     decode-shaped packs, several workgroups per CU);
+//     VALU work runs beside another wave's MFMAs; 8 at 256; 4 at 64; small tiles for packs of short sequences: 4
+//     waves, three workgroups per CU at 128, two at 256), or a workgroup is one wave (narrow tiles for decode-shaped
+//     packs, several workgroups per CU);
 //   * per step, BN keys of K and V are copied global -> LDS by the DMA path (buffer_load ... lds, 16 B per lane),
 //     double buffered, the next step's copy in flight while this step computes;
 //   * S^T = K Q^T on v_mfma_f32_32x32x16_bf16: a lane owns one query column, so the row max and sum are in-lane plus
@@ -43,21 +44,20 @@ namespace karpo {
 
 // Lazy-rescale threshold in log2 units: P values stay below 2^8.
 constexpr float kTau = 8.0f;
-// Per head size and tile shape: keys per step (BN) and waves per SIMD the registers are budgeted for (OCC).
-// Wide: D=64 4-wave workgroups, four per CU; D=128 one 12-wave workgroup per CU (three waves per SIMD) sharing one
-// 64-key K/V stream, 64 KiB LDS; D=256 one 8-wave workgroup per CU, 64 KiB LDS; D=512 one 8-wave workgroup (four
-// pairs, two waves per SIMD), 128 KiB LDS. Narrow: one wave per workgroup (a pair at D=512), 32 KiB LDS (64 KiB at
-// D=256, 128 KiB at D=512), LDS-limited to five (two, one) per CU.
-#ifndef KA_OCC128
-#define KA_OCC128 3
-#endif
-#ifndef KA_OCC256
-#define KA_OCC256 2
-#endif
-template <int D, bool NARROW> struct TileCfg {
-  static constexpr int W = tile_waves(D, NARROW);
-  static constexpr int BN = tile_keys(D, NARROW);
-  static constexpr int OCC = NARROW ? (D >= 256 ? 1 : 2) : D == 512 ? 2 : D == 64 ? 4 : D == 128 ? KA_OCC128 : KA_OCC256;
+// Per head size and tile shape (TileShape of plan_common.h): waves (W), keys per step (BN) and waves per SIMD the
+// registers are budgeted for (OCC). Wide: D=64 4-wave workgroups, four per CU; D=128 one 12-wave workgroup per CU
+// (three waves per SIMD) sharing one 32-key K/V stream (64-key steps in the long shape), 32 KiB LDS (64 KiB); D=256
+// one 8-wave workgroup per CU, 64 KiB LDS; D=512 one 8-wave workgroup (four pairs, two waves per SIMD), 128 KiB LDS.
+// Small: 4-wave workgroups, three per CU at D=128 (32 KiB LDS each), two at D=256 (64 KiB). Narrow: one wave per
+// workgroup (a pair at D=512), 32 KiB LDS (64 KiB at D=256, 128 KiB at D=512), LDS-limited to five (two, one) per CU.
+template <int D, int SHAPE> struct TileCfg {
+  static constexpr int W = tile_waves(D, SHAPE);
+  static constexpr int BN = tile_keys(D, SHAPE);
+  static constexpr int OCC = SHAPE == kNarrow ? (D >= 256 ? 1 : 2)
+                             : D == 512       ? 2
+                             : D == 64        ? 4
+                             : D == 128       ? 3
+                                              : 2;
   static constexpr bool PAIR = D == 512;  // a pair of waves per 32 query vectors, each with half of D
 };
 
@@ -215,11 +215,11 @@ __device__ __forceinline__ u32x2 output4(const Params& p, float o0, float o1, fl
   return w;
 }
 
-template <int D, bool NARROW, bool GATHER>
-__global__ __launch_bounds__((64 * TileCfg<D, NARROW>::W), (TileCfg<D, NARROW>::OCC)) void attn_fwd_kernel(Params p) {
-  constexpr int W = TileCfg<D, NARROW>::W;  // waves of the workgroup
-  constexpr int BN = TileCfg<D, NARROW>::BN;
-  constexpr bool PAIR = TileCfg<D, NARROW>::PAIR;
+template <int D, int SHAPE, bool GATHER>
+__global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OCC)) void attn_fwd_kernel(Params p) {
+  constexpr int W = TileCfg<D, SHAPE>::W;  // waves of the workgroup
+  constexpr int BN = TileCfg<D, SHAPE>::BN;
+  constexpr bool PAIR = TileCfg<D, SHAPE>::PAIR;
   constexpr int DC = D / 16;       // 16-wide head-dim chunks of the QK^T contraction
   constexpr int DB = D / 32;       // 32-row head-dim blocks of O^T
   constexpr int QC = PAIR ? DC / 2 : DC;  // chunks of Q this wave holds (half of D in a pair)
@@ -571,7 +571,7 @@ __global__ __launch_bounds__((64 * TileCfg<D, NARROW>::W), (TileCfg<D, NARROW>::
   // ---- store: lane (col, half) holds d = db*32 + (j/4)*8 + half*4 + j%4 of its query vector
   const float lt = half_swap_sum(l);
   if (parts > 1) {  // one part of a split tile: unnormalised fp32 O, m and l for merge_kernel
-    constexpr int V = tile_vectors(D, NARROW);
+    constexpr int V = tile_vectors(D, SHAPE);
     float* base = p.partial + ((int64_t)(slot + part) * p.n_hg + hg) * (int64_t)V * (D + 2);
     float* op = base + (int64_t)vec * D + dh * (D / 2) + half * 4;
 #pragma unroll
@@ -907,19 +907,20 @@ hipError_t launch_norm_rope(const NormRopeParams& p, int head_dim, hipStream_t s
 
 // ---- launch
 
-template <int D, bool NARROW>
+template <int D, int SHAPE>
 static hipError_t launch_attn(const Params& p, int64_t items, int64_t merges, int n_hg, hipStream_t stream) {
+  using Cfg = TileCfg<D, SHAPE>;
   if (p.k_rows != nullptr)
-    hipLaunchKernelGGL((attn_fwd_kernel<D, NARROW, true>), dim3((unsigned)(items * n_hg)),
-                       dim3(64 * TileCfg<D, NARROW>::W), 0, stream, p);
+    hipLaunchKernelGGL((attn_fwd_kernel<D, SHAPE, true>), dim3((unsigned)(items * n_hg)), dim3(64 * Cfg::W), 0,
+                       stream, p);
   else
-    hipLaunchKernelGGL((attn_fwd_kernel<D, NARROW, false>), dim3((unsigned)(items * n_hg)),
-                       dim3(64 * TileCfg<D, NARROW>::W), 0, stream, p);
+    hipLaunchKernelGGL((attn_fwd_kernel<D, SHAPE, false>), dim3((unsigned)(items * n_hg)), dim3(64 * Cfg::W), 0,
+                       stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || merges <= 0) return e;
-  constexpr int64_t per_merge = (int64_t)tile_vectors(D, NARROW) * (D / 4);  // threads of one head group
+  constexpr int64_t per_merge = (int64_t)tile_vectors(D, SHAPE) * (D / 4);  // threads of one head group
   const int64_t blocks = (merges * n_hg * per_merge + kMergeThreads - 1) / kMergeThreads;
-  hipLaunchKernelGGL((merge_kernel<D, TileCfg<D, NARROW>::W>), dim3((unsigned)(blocks < kMergeBlocks ? blocks : kMergeBlocks)),
+  hipLaunchKernelGGL((merge_kernel<D, Cfg::W>), dim3((unsigned)(blocks < kMergeBlocks ? blocks : kMergeBlocks)),
                      dim3(kMergeThreads), 0, stream, p);
   return hipGetLastError();
 }
@@ -927,15 +928,18 @@ static hipError_t launch_attn(const Params& p, int64_t items, int64_t merges, in
 hipError_t launch_forward(const Params& p, int head_dim, const Geometry& g, int64_t items, int64_t merges,
                           hipStream_t stream) {
   if (items <= 0) return hipSuccess;
-  switch (head_dim * 2 + (g.narrow ? 1 : 0)) {
-    case 128: return launch_attn<64, false>(p, items, merges, g.n_hg, stream);
-    case 129: return launch_attn<64, true>(p, items, merges, g.n_hg, stream);
-    case 256: return launch_attn<128, false>(p, items, merges, g.n_hg, stream);
-    case 257: return launch_attn<128, true>(p, items, merges, g.n_hg, stream);
-    case 512: return launch_attn<256, false>(p, items, merges, g.n_hg, stream);
-    case 513: return launch_attn<256, true>(p, items, merges, g.n_hg, stream);
-    case 1024: return launch_attn<512, false>(p, items, merges, g.n_hg, stream);
-    case 1025: return launch_attn<512, true>(p, items, merges, g.n_hg, stream);
+  switch (head_dim * 4 + g.shape) {  // the shapes tile_shape selects per head size
+    case 64 * 4 + kWide: return launch_attn<64, kWide>(p, items, merges, g.n_hg, stream);
+    case 64 * 4 + kNarrow: return launch_attn<64, kNarrow>(p, items, merges, g.n_hg, stream);
+    case 128 * 4 + kWide: return launch_attn<128, kWide>(p, items, merges, g.n_hg, stream);
+    case 128 * 4 + kNarrow: return launch_attn<128, kNarrow>(p, items, merges, g.n_hg, stream);
+    case 128 * 4 + kSmall: return launch_attn<128, kSmall>(p, items, merges, g.n_hg, stream);
+    case 128 * 4 + kLong: return launch_attn<128, kLong>(p, items, merges, g.n_hg, stream);
+    case 256 * 4 + kWide: return launch_attn<256, kWide>(p, items, merges, g.n_hg, stream);
+    case 256 * 4 + kNarrow: return launch_attn<256, kNarrow>(p, items, merges, g.n_hg, stream);
+    case 256 * 4 + kSmall: return launch_attn<256, kSmall>(p, items, merges, g.n_hg, stream);
+    case 512 * 4 + kWide: return launch_attn<512, kWide>(p, items, merges, g.n_hg, stream);
+    case 512 * 4 + kNarrow: return launch_attn<512, kNarrow>(p, items, merges, g.n_hg, stream);
     default: return hipErrorInvalidValue;
   }
 }

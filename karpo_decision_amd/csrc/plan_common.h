@@ -7,10 +7,17 @@
 // key/value head, so one staged K/V tile serves every head of the group; otherwise it covers `vectors` positions of
 // one query head.
 //
-// Two tile shapes per head size:
-//   * wide (prefill): several waves share one K/V stream (12 at head_dim 128, 8 at 256 and 512, 4 at 64);
+// Tile shapes, chosen per call from the longest query run (tile_shape):
+//   * wide (prefill): several waves share one K/V stream (12 at head_dim 128, 8 at 256 and 512, 4 at 64), 32-key
+//     steps (64 at head_dim 64);
+//   * long (head_dim 128, runs above 65,536 queries): the wide tile with 64-key steps;
+//   * small (head_dim 128 runs up to 4,096 queries, 256 up to 8,192): 4-wave workgroups, three (two) per CU, so a
+//     pack of short sequences has three (two) times the work items to balance over the CUs;
 //   * narrow (decode-shaped packs, every sequence's queries fit one wave's 32 vectors, e.g. the markers-only layer
 //     with one query per sequence): one wave per workgroup (one pair at head_dim 512), several per CU.
+// The thresholds are measured (one box, interleaved runs): 32-key wide steps against 64 are -5% at a 32k causal
+// sequence and -7% on the 65k multimodal pack but +5% at 131k; small tiles are -17% on the Qwen pack (longest run
+// 2,210) and -6% on the branched block plan (4,096), +12% at 131k.
 // A tile whose key steps exceed the pack's per-workgroup share is split into parts over its key steps; each part
 // writes an fp32 partial (O, running max, sum) and a merge kernel combines them. This bounds the critical path of
 // small packs (few long tiles) and gives decode-shaped packs the parallelism of their keys.
@@ -25,31 +32,29 @@
 
 namespace karpo {
 
-#ifndef KA_W128
-#define KA_W128 12
-#endif
-#ifndef KA_W256
-#define KA_W256 8
-#endif
-#ifndef KA_BN128
-#define KA_BN128 64
-#endif
-// Waves per workgroup (each holds 32 query vectors of the tile), keys per step and workgroups resident per CU (the
-// register and LDS budget of the kernel), per head size and tile shape.
-KA_HD constexpr int tile_waves(int head_dim, bool narrow) {
-  return head_dim == 512 ? (narrow ? 2 : 8) : narrow ? 1 : head_dim == 128 ? KA_W128 : head_dim == 256 ? KA_W256 : 4;
+enum TileShape : int { kWide = 0, kNarrow = 1, kSmall = 2, kLong = 3 };
+
+// Waves per workgroup (each holds 32 query vectors of the tile, a pair of waves at head_dim 512), keys per step and
+// workgroups resident per CU (the register and LDS budget of the kernel), per head size and tile shape.
+KA_HD constexpr int tile_waves(int head_dim, int shape) {
+  return shape == kNarrow ? (head_dim == 512 ? 2 : 1)
+         : shape == kSmall ? 4
+         : head_dim == 512 ? 8 : head_dim == 128 ? 12 : head_dim == 256 ? 8 : 4;
 }
 // Query vectors per tile: 32 per wave, or per pair of waves at head_dim 512 (each wave of a pair holds half of every
 // vector's elements: half of Q's operands and of O's accumulators).
-KA_HD constexpr int tile_vectors(int head_dim, bool narrow) {
-  return 32 * tile_waves(head_dim, narrow) / (head_dim == 512 ? 2 : 1);
+KA_HD constexpr int tile_vectors(int head_dim, int shape) {
+  return 32 * tile_waves(head_dim, shape) / (head_dim == 512 ? 2 : 1);
 }
-KA_HD constexpr int tile_keys(int head_dim, bool narrow) {
-  return head_dim == 64 ? 64 : head_dim >= 256 ? 32 : narrow ? 32 : KA_BN128;
+KA_HD constexpr int tile_keys(int head_dim, int shape) {
+  return head_dim == 64 ? 64 : head_dim >= 256 ? 32 : shape == kLong ? 64 : 32;
 }
-KA_HD constexpr int tiles_per_cu(int head_dim, bool narrow) {
-  // two K and two V tiles of tile_keys x head_dim bf16 per workgroup in 160 KiB of LDS (narrow: one wave each)
-  return narrow ? (head_dim == 512 ? 1 : head_dim == 256 ? 2 : 5) : head_dim == 64 ? 4 : 1;
+// Workgroups per CU the split policy plans for (its concurrency): the resident ones (two K and two V tiles of
+// tile_keys x head_dim bf16 per workgroup in 160 KiB of LDS, and the registers), except small tiles, planned one per CU
+// although two or three run there: splitting to the per-workgroup share made more split parts than their merge repays
+// (Qwen pack 0.110 against 0.097 ms).
+KA_HD constexpr int tiles_per_cu(int head_dim, int shape) {
+  return shape == kNarrow ? (head_dim == 512 ? 1 : head_dim == 256 ? 2 : 5) : head_dim == 64 ? 4 : 1;
 }
 constexpr int kComputeUnits = 256;   // MI355X
 constexpr int kPlanHeader = 8;       // int32 header of a plan (see karpo_attn.h)
@@ -59,7 +64,7 @@ constexpr int kCostBuckets = 2048;   // device planner's cost histogram (costs c
 constexpr int kMinSplitSteps = 8;    // only tiles longer than this split (a merge costs a few steps' time)
 
 struct Geometry {
-  bool narrow;   // one-wave tiles
+  int shape;     // TileShape
   int waves;     // waves per workgroup
   int vectors;   // query vectors per tile
   int bn;        // keys per step
@@ -71,24 +76,30 @@ struct Geometry {
 
 KA_HD inline bool head_dim_supported(int d) { return d == 64 || d == 128 || d == 256 || d == 512; }
 
-KA_HD inline Geometry geometry_of(int heads, int kv_heads, int head_dim, bool narrow) {
+KA_HD inline Geometry geometry_of(int heads, int kv_heads, int head_dim, int shape) {
   Geometry g;
-  g.narrow = narrow;
-  g.waves = tile_waves(head_dim, narrow);
-  g.vectors = tile_vectors(head_dim, narrow);
-  g.bn = tile_keys(head_dim, narrow);
+  g.shape = shape;
+  g.waves = tile_waves(head_dim, shape);
+  g.vectors = tile_vectors(head_dim, shape);
+  g.bn = tile_keys(head_dim, shape);
   const int group = heads / kv_heads;
   g.ng = (g.vectors % group == 0) ? group : 1;
   g.rows = g.vectors / g.ng;
   g.n_hg = heads / g.ng;
-  g.conc = kComputeUnits * tiles_per_cu(head_dim, narrow);
+  g.conc = kComputeUnits * tiles_per_cu(head_dim, shape);
   return g;
 }
 
-// The narrow shape when every sequence's queries (max_q) fit one narrow tile, else the wide one.
+// The tile shape for a pack whose longest query run is max_q: narrow when every sequence's queries fit one narrow
+// tile; small for short runs at head_dim 128 and 256; long for very long runs at 128; else wide.
+KA_HD inline int tile_shape(int heads, int kv_heads, int head_dim, int64_t max_q) {
+  if (max_q <= geometry_of(heads, kv_heads, head_dim, kNarrow).rows) return kNarrow;
+  if ((head_dim == 128 && max_q <= 4096) || (head_dim == 256 && max_q <= 8192)) return kSmall;
+  if (head_dim == 128 && max_q > 65536) return kLong;
+  return kWide;
+}
 KA_HD inline Geometry geometry(int heads, int kv_heads, int head_dim, int64_t max_q) {
-  const Geometry n = geometry_of(heads, kv_heads, head_dim, true);
-  return max_q <= n.rows ? n : geometry_of(heads, kv_heads, head_dim, false);
+  return geometry_of(heads, kv_heads, head_dim, tile_shape(heads, kv_heads, head_dim, max_q));
 }
 
 KA_HD inline int64_t ka_min(int64_t a, int64_t b) { return a < b ? a : b; }
@@ -153,7 +164,7 @@ KA_HD constexpr int bwd_tile_vectors(int head_dim, bool key_tiles) {
 // key/value head per item; the planner sees keys as queries and query rows as keys).
 KA_HD inline Geometry bwd_geometry(int heads, int kv_heads, int head_dim, bool key_tiles) {
   Geometry g;
-  g.narrow = false;
+  g.shape = kWide;
   g.waves = key_tiles ? kBwdWaves : bwd_q_waves(head_dim);
   g.vectors = bwd_tile_vectors(head_dim, key_tiles);
   g.bn = key_tiles ? kBwdStep : bwd_q_step(head_dim);

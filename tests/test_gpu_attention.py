@@ -324,13 +324,16 @@ def _plan_parts(plan: torch.Tensor) -> tuple[list[int], list[tuple], list[tuple]
 def test_every_row_is_written_and_device_plan_matches_host_plan(gpu):
     """Through the C ABI: an output pre-filled with NaN has no NaN left; the device planner's work list is the host
     planner's (same header and split tiles, the same items as a multiset, ordered by non-increasing cost); running
-    from the host plan gives the same bits. The Qwen-class pack is small enough that its longest tiles split."""
+    from the host plan gives the same bits. The Qwen-class pack in the wide tile shape (max_q 8192: above the small
+    shape's runs) is small enough that its longest tiles split."""
     w = workloads.qwen_full(gpu, seed=7)
     q_cu = torch.tensor(w.q_cu, dtype=torch.int32, device=gpu)
+    max_q = 8192
     o = torch.full_like(w.query, float("nan"))
-    ws = _c_abi_call(w.query, w.key, w.value, o, q_cu, q_cu, w.max_q, w.scale, -1, 0)
+    ws = _c_abi_call(w.query, w.key, w.value, o, q_cu, q_cu, max_q, w.scale, -1, 0)
     assert not torch.isnan(o).any()
-    plan = ops.make_plan(w.q_cu, w.k_cu, w.heads, w.kv_heads, w.head_dim, -1, 0, device=gpu)
+    plan = ops.make_plan(w.q_cu, w.k_cu, w.heads, w.kv_heads, w.head_dim, -1, 0, device=gpu, max_q=max_q)
+    assert plan.header[5] == 12
     host_header, host_merges, host_items = _plan_parts(plan.tensor)
     dev_header, dev_merges, dev_items = _plan_parts(ws.view(torch.int32)[: plan.tensor.numel()])
     assert host_header[4] > 0, "expected split tiles in this pack"
@@ -347,7 +350,7 @@ def test_every_row_is_written_and_device_plan_matches_host_plan(gpu):
         costs.append(-(-steps // parts) + 1)
     assert all(a >= b for a, b in zip(costs, costs[1:]))
     o2 = torch.empty_like(w.query)
-    _c_abi_call(w.query, w.key, w.value, o2, q_cu, q_cu, w.max_q, w.scale, -1, 0, plan=plan.tensor)
+    _c_abi_call(w.query, w.key, w.value, o2, q_cu, q_cu, max_q, w.scale, -1, 0, plan=plan.tensor)
     assert torch.equal(o, o2)
 
 

@@ -60,7 +60,8 @@ def host_plan(q_cu, k_cu, heads, kv_heads, head_dim, left, right, max_q=_lib.LON
     return header, merges, items
 
 
-#: Workgroups one CU runs at once, per (head_dim, one-wave tiles): the register and LDS budgets of the kernels.
+#: Workgroups per CU the split policy plans for, per (head_dim, one-wave tiles): the register and LDS budgets of the
+#: kernels (small tiles, 4 waves at head_dim 128 / 256, are planned one per CU like the wide ones).
 TILES_PER_CU = {(64, False): 4, (128, False): 1, (256, False): 1, (512, False): 1, (64, True): 5, (128, True): 5,
                 (256, True): 2, (512, True): 1}
 GEOMETRIES = [(8, 2, 64), (16, 8, 128), (32, 16, 128), (16, 8, 256), (12, 4, 128), (10, 2, 128), (4, 4, 64),
@@ -136,16 +137,26 @@ def test_markers_plan_splits_keys():
 
 def test_tile_geometry():
     # a tile holds 32 query vectors per wave (12 waves at head_dim 128, 8 at 256, 4 at 64); the GQA group's heads
-    # share it when they divide it
+    # share it when they divide it. Head size 128: 32-key steps, 64 for runs above 65,536 queries
+    assert _lib.tile_shape(32, 16, 128, 32768) == (192, 32, 2)
+    assert _lib.tile_shape(32, 16, 128, 65536) == (192, 32, 2)
+    assert _lib.tile_shape(32, 16, 128, 65537) == (192, 64, 2)
     assert _lib.tile_shape(32, 16, 128) == (192, 64, 2)
     assert _lib.tile_shape(8, 2, 64) == (32, 64, 4)
     assert _lib.tile_shape(16, 8, 256) == (128, 32, 2)
     assert _lib.tile_shape(12, 4, 128) == (128, 64, 3)  # a group of 3 divides 384 vectors
     assert _lib.tile_shape(10, 2, 128) == (384, 64, 1)  # a group of 5 does not: one head per item
+    # small tiles (4 waves) for runs up to 4,096 queries at head size 128 and 8,192 at 256
+    assert _lib.tile_shape(32, 16, 128, 4096) == (64, 32, 2)
+    assert _lib.tile_shape(32, 16, 128, 4097) == (192, 32, 2)
+    assert _lib.tile_shape(16, 8, 256, 8192) == (64, 32, 2)
+    assert _lib.tile_shape(16, 8, 256, 8193) == (128, 32, 2)
+    assert _lib.tile_shape(12, 4, 128, 1000) == (128, 32, 1)  # a group of 3 does not divide 128 vectors
+    assert _lib.tile_shape(8, 2, 64, 1000) == (32, 64, 4)  # head size 64: the wide tile is already 4 waves
     # one-wave tiles when every sequence's queries fit 32 vectors
     assert _lib.tile_shape(32, 16, 128, 1) == (16, 32, 2)
     assert _lib.tile_shape(32, 16, 128, 16) == (16, 32, 2)
-    assert _lib.tile_shape(32, 16, 128, 17) == (192, 64, 2)
+    assert _lib.tile_shape(32, 16, 128, 17) == (64, 32, 2)
     assert _lib.tile_shape(32, 4, 256, 4) == (4, 32, 8)
     assert _lib.tile_shape(8, 2, 64, 8) == (8, 64, 4)
     assert _lib.tile_shape(10, 2, 128, 32) == (32, 32, 1)
@@ -271,12 +282,17 @@ def test_workspace_and_capacity():
 
 
 def test_python_plan_object():
-    plan = ops.make_plan([0, 100, 400], [0, 100, 400], 32, 16, 128, -1, 0, device="cpu")
+    # max_q above 65,536: the 12-wave tiles with 64-key steps
+    plan = ops.make_plan([0, 100, 400], [0, 100, 400], 32, 16, 128, -1, 0, device="cpu", max_q=70000)
     # tiles of 2, 3 and 5 key steps, none longer than the shortest split (8 steps)
     assert plan.items == 3 and plan.rows_per_tile == 192 and plan.split_tiles == 0
     assert plan.tensor.dtype.is_signed and plan.tensor.numel() == 8 + 4 * plan.items
     assert plan.header == [3, 192, 64, 2, 0, 12, 8, 0]
-    long = ops.make_plan([0, 3000], [0, 3000], 32, 16, 128, -1, 0, device="cpu")
+    # the default max_q (the longest run, 300): small tiles of 64 rows, 32-key steps, 4 waves; tiles of 2, 4 and 2, 4,
+    # 6, 8, 10 steps: the 10-step tile is longer than the shortest split and takes two parts
+    small = ops.make_plan([0, 100, 400], [0, 100, 400], 32, 16, 128, -1, 0, device="cpu")
+    assert small.header[1:6] == [64, 32, 2, 1, 4] and small.items == 2 + 5 + 1
+    long = ops.make_plan([0, 3000], [0, 3000], 32, 16, 128, -1, 0, device="cpu", max_q=70000)
     # 16 tiles of 3, 6, .., 45 and 47 steps: 407 x 16 = 6512 workgroup-steps over 256, parts of at most 26 steps
     assert long.split_tiles == 8 and long.items == 16 + 8
     with pytest.raises(ValueError):
