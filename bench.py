@@ -238,8 +238,10 @@ def backward(args, device, w) -> int:
                    "flops_per_step": flops, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
-                     "kernel": f"karpo_attn_bwd (bwd_stats_kernel, bwd_dq_kernel<{w.head_dim}>, "
-                               f"bwd_dkdv_kernel<{w.head_dim}, *>)",
+                     "kernel": (f"karpo_attn_bwd (bwd_stats_kernel, bwd_dq_pair_kernel<512>, bwd_dkdv_pair_kernel<512>)"
+                                if w.head_dim == 512 else
+                                f"karpo_attn_bwd (bwd_stats_kernel, bwd_dq_kernel<{w.head_dim}>, "
+                                f"bwd_dkdv_kernel<{w.head_dim}, *>)"),
                      "avg_launch_ms": round(launch_ms, 4)},
     }
     if not args.no_cpu_baseline:
@@ -316,8 +318,7 @@ def main() -> int:
         entry = json.loads(TRAFFIC.read_text()).get(w.name)
         if entry:
             traffic = entry.get("bytes_per_launch")
-    rows, _, per = _lib.tile_shape(w.heads, w.kv_heads, w.head_dim, w.max_q)
-    narrow = rows * per == 32
+    shape = _lib.kernel_shape(w.heads, w.kv_heads, w.head_dim, w.max_q)
     if w.bound(PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)) == "mfma":
         roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_BF16_TFLOPS, 4)}
@@ -335,7 +336,8 @@ def main() -> int:
                    "tokens_per_s": round(w.tokens / (ms_per_step * 1e-3)), "flops_per_step": flops,
                    "min_hbm_bytes_per_step": w.bytes(), "parallelism": "single GPU"},
         "roofline": {**roof, "traffic": traffic,
-                     "kernel": f"attn_fwd_kernel<{w.head_dim}, {str(narrow).lower()}, {str(rows is not None).lower()}>",
+                     "kernel": f"attn_fwd_kernel<{w.head_dim}, {shape}, "
+                               f"{str(rows is not None and not args.materialize_gather).lower()}>",
                      "avg_launch_ms": round(launch_ms, 4)},
     }
     if not args.no_cpu_baseline:

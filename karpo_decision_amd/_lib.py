@@ -124,6 +124,22 @@ def check(status: int, what: str) -> None:
 LONG = 1 << 30
 
 
+def kernel_shape(heads: int, kv_heads: int, head_dim: int, max_q: int = LONG) -> int:
+    """The forward kernel's tile-shape template argument for these heads and longest query run (0 wide, 1 narrow: one
+    wave, or one pair at head_dim 512; 2 small: four waves at head_dim 128 / 256; 3 long: 64-key steps at 128), as
+    read off tile_shape's geometry."""
+    rows, keys, per = tile_shape(heads, kv_heads, head_dim, max_q)
+    vectors = rows * per
+    waves = vectors // 32 * (2 if head_dim == 512 else 1)
+    if vectors == 32:
+        return 1
+    if head_dim in (128, 256) and waves == 4:
+        return 2
+    if head_dim == 128 and keys == 64:
+        return 3
+    return 0
+
+
 def tile_shape(heads: int, kv_heads: int, head_dim: int, max_q: int = LONG) -> tuple[int, int, int]:
     """(query rows per tile, keys per step, query heads per work item) for packs whose longest query run is
     ``max_q`` (one-wave tiles when every run fits one)."""

@@ -164,6 +164,10 @@ def test_tile_geometry():
     assert _lib.tile_shape(32, 4, 512) == (16, 32, 8)
     assert _lib.tile_shape(32, 4, 512, 4) == (4, 32, 8)
     assert _lib.tile_shape(6, 2, 512) == (128, 32, 1)  # a group of 3 does not divide 128 vectors
+    # the kernels' shape numbering (wide 0, narrow 1, small 2, long 3), as bench.py labels the launch
+    assert [_lib.kernel_shape(32, 16, 128, n) for n in (32768, 16, 4096, 65537)] == [0, 1, 2, 3]
+    assert [_lib.kernel_shape(16, 8, 256, n) for n in (16384, 8192)] == [0, 2]
+    assert [_lib.kernel_shape(32, 4, 512, n) for n in (32768, 4)] == [0, 1]
 
 
 def test_plan_refuses_bad_bounds_and_small_buffers():
