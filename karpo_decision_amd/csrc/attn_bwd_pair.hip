@@ -1,16 +1,18 @@
 // The backward at head size 512 (the 31B global layers) for gfx950: the arithmetic of attn_bwd.hip, with pairs of
-// waves sharing 32 query vectors (dQ kernel) or 32 keys (dK, dV kernels) as the forward's 512 tiles do. One wave
+// waves sharing 32 query vectors (dQ kernel) or 32 keys (dK / dV kernel) as the forward's 512 tiles do. One wave
 // cannot hold a 512-wide operand row and accumulator row for 32 vectors (128 + 256 registers per lane for each), so
 // each wave of a pair holds half of D: half of the operands in registers and half of the gradient accumulators. A
-// step's S (and dP) is a sum over all of D: each wave computes the product over its half, the pair adds the two
-// partials through LDS (low half + high half, in that order in both waves, so both hold bit-equal sums), both run the
-// same softmax, and each accumulates its half of the gradient.
+// step's S (and dP) is a sum over all of D: each wave computes the product over its half and the pair adds the two
+// partials through LDS (low half + high half, in that order, so the sums are bit-equal wherever they are formed).
 //
-// A step has two barriers: (1) after the S / dP products (the partials are written), (2) at its end. The tile a step
-// reads in both halves of the step (K for dQ, Q for dK and dV; S layout, read as rows and transposed) has two
-// buffers: the next step's is copied from the step's start, a whole step ahead of its use. dV's transposed dO has two
-// buffers as well. The row tile read only by the products before barrier 1 (V for dQ, dO for dK) has one buffer,
-// refilled for the next step right after barrier 1. 32 KiB per tile and buffer.
+// dQ kernel: both waves of a pair add the whole step's partials and run the same softmax; two barriers per step, (1)
+// after the S / dP products (the partials are written), (2) at its end. K, read as rows and transposed (S layout),
+// has two buffers: the next step's is copied from the step's start, a whole step ahead of its use; V, read only by
+// the products before barrier 1, has one, refilled for the next step right after barrier 1.
+// dK / dV kernel: both gradients in one pass over Q and dO (both read as rows and transposed, two buffers each). The
+// pair splits the softmax by row block, each wave receiving only the partner's partials of its 16 rows, and the two
+// swap P and dS as bf16 MFMA operands: three barriers per step (partials written, P / dS written, end).
+// 32 KiB per tile and buffer.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -27,23 +29,14 @@ constexpr int kPairWaves = 4;  // two pairs per workgroup
 constexpr int kPairStep = 32;  // keys (dQ) or query rows (dK, dV) per step
 
 // A wave's eight 1 KiB copy blocks per tile (blocks 8w .. 8w+7 of 32) at head size 512, as byte offsets from the
-// tile's first row (s_dma_source / v_dma_source of block 8w + r): the S layout's advance 64 B per block; the
-// transposed layout's advance 256 B per block, and four rows further from block 4 on. One or two registers per layout
-// instead of eight (checked against the per-block formulas for every wave, lane and block).
+// tile's first row (s_dma_source of block 8w + r): they advance 64 B per block, so one register per tile holds them
+// instead of eight (checked against the per-block formula for every wave, lane and block).
 __device__ __forceinline__ uint32_t s_block_base(int wave, int lane, int64_t stride) {
   int row, colm;
   s_dma_source<512>(wave * 8, lane, &row, &colm);
   return (uint32_t)(row * stride + colm) * 2u;
 }
-__device__ __forceinline__ uint32_t v_block_base(int wave, int lane, int64_t stride) {
-  int key, colm;
-  v_dma_source<512>(wave * 8, lane, &key, &colm);
-  return (uint32_t)(key * stride + colm) * 2u;
-}
 __device__ __forceinline__ uint32_t s_block(uint32_t base, int r) { return base + (uint32_t)r * 64u; }
-__device__ __forceinline__ uint32_t v_block(uint32_t base, int64_t stride, int r) {
-  return base + (uint32_t)(r >> 2) * (uint32_t)(8 * stride) + (uint32_t)(r & 3) * 256u;
-}
 
 // The pair's partial S (q4 0-3) and dP (q4 4-7) of one wave: 32 floats per lane as 8 f32x4 [q4][lane].
 __device__ __forceinline__ void exchange_write(KA_LDS f32x4* slot, int lane, const f32x16& a, const f32x16& b,
