@@ -6,7 +6,7 @@
 //   dV = P^T dO,  dP = dO V^T,  dS = P * (dP - D),  dQ = scale * dS K,  dK = scale * dS^T Q.
 // P and dS enter the MFMAs as bf16 (as P does in the forward), every product accumulates in fp32.
 //
-// Three kernels after the two planners (plan_kernel of attn_fwd.hip, no split tiles):
+// Three kernels after the planner (plan_kernel of attn_fwd.hip: both work lists in one launch, no split tiles):
 //   * bwd_stats_kernel: per (head, query row) the log2-domain LSE (+inf for a row that sees no key, so its P are 0)
 //     and D;
 //   * bwd_dq_kernel (query-stationary, the forward's tiles): Q and dO of 32 query vectors per wave as MFMA B operands
@@ -646,14 +646,12 @@ static hipError_t launch_bwd_d(const BwdParams& p, const Geometry& gq, const Geo
 
 hipError_t launch_bwd(const BwdParams& p, int head_dim, const Geometry& gq, const Geometry& gk, int32_t* plan_q,
                       int32_t* plan_k, int64_t items_q, int64_t items_k, int tiles_q, int merges_q, int tiles_k,
-                      int merges_k, int32_t* tile_base, int n_seq, hipStream_t stream) {
-  // the two work lists: query tiles as the forward's, key tiles from the bounds swapped (a key j sees query rows
-  // i with j - right <= i + delta <= j + left: the window mirrored)
-  hipError_t e = launch_plan(p.q_cu, p.k_cu, n_seq, gq, p.left, p.right, plan_q, tiles_q, merges_q, (int)items_q,
-                             tile_base, stream);
-  if (e != hipSuccess) return e;
-  e = launch_plan(p.k_cu, p.q_cu, n_seq, gk, p.right, p.left, plan_k, tiles_k, merges_k, (int)items_k, tile_base,
-                  stream);
+                      int merges_k, int32_t* tile_base_q, int32_t* tile_base_k, int n_seq, hipStream_t stream) {
+  // the two work lists, in one planner launch: query tiles as the forward's, key tiles from the bounds swapped (a
+  // key j sees query rows i with j - right <= i + delta <= j + left: the window mirrored)
+  const PlanJob jobs[2] = {{p.q_cu, p.k_cu, gq, p.left, p.right, plan_q, tiles_q, merges_q, (int)items_q, tile_base_q},
+                           {p.k_cu, p.q_cu, gk, p.right, p.left, plan_k, tiles_k, merges_k, (int)items_k, tile_base_k}};
+  hipError_t e = launch_plan(jobs, 2, n_seq, stream);
   if (e != hipSuccess) return e;
   switch (head_dim) {
     case 64: return launch_bwd_d<64>(p, gq, gk, plan_q, plan_k, items_q, items_k, stream);

@@ -709,12 +709,19 @@ __device__ int64_t block_sum64(int64_t x, int64_t* scratch /* >= kPlanThreads/64
 // The plan of karpo_attn.h from the device bounds, in three passes over the tiles: the pack's workgroup-steps (which
 // set the split length), a histogram of part costs, and the scatter (descending cost order; split tiles' slots and
 // merge entries in tile order). The host planner (plan.cpp) lists the same items; among equal costs the order here
-// depends on atomics.
-__global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int32_t* __restrict__ q_cu,
-                                                            const int32_t* __restrict__ k_cu, int n_seq,
-                                                            Geometry g, int left, int right,
-                                                            int32_t* __restrict__ plan, int tiles_cap, int merges_cap,
-                                                            int items_cap, int32_t* __restrict__ tile_base) {
+// depends on atomics. Workgroup b plans job b (the backward's two work lists in one launch).
+struct PlanJobs {
+  PlanJob a, b;
+};
+__global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanJobs jobs, int n_seq) {
+  const PlanJob job = blockIdx.x == 0 ? jobs.a : jobs.b;
+  const int32_t* __restrict__ q_cu = job.q_cu;
+  const int32_t* __restrict__ k_cu = job.k_cu;
+  const Geometry g = job.g;
+  const int left = job.left, right = job.right;
+  int32_t* __restrict__ plan = job.plan;
+  const int tiles_cap = job.tiles, merges_cap = job.merges, items_cap = job.items;
+  int32_t* __restrict__ tile_base = job.tile_base;
   __shared__ int hist[kCostBuckets];
   __shared__ int scratch[kPlanThreads / 64 + 1];
   __shared__ int64_t scratch64[kPlanThreads / 64];
@@ -944,10 +951,10 @@ hipError_t launch_forward(const Params& p, int head_dim, const Geometry& g, int6
   }
 }
 
-hipError_t launch_plan(const int32_t* q_cu, const int32_t* k_cu, int n_seq, const Geometry& g, int left, int right,
-                       int32_t* plan, int tiles, int merges, int items, int32_t* tile_base, hipStream_t stream) {
-  hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, q_cu, k_cu, n_seq, g, left, right, plan,
-                     tiles, merges, items, tile_base);
+hipError_t launch_plan(const PlanJob* jobs, int n_jobs, int n_seq, hipStream_t stream) {
+  if (n_jobs < 1 || n_jobs > 2) return hipErrorInvalidValue;
+  const PlanJobs pj = {jobs[0], jobs[n_jobs - 1]};
+  hipLaunchKernelGGL(plan_kernel, dim3((unsigned)n_jobs), dim3(kPlanThreads), 0, stream, pj, n_seq);
   return hipGetLastError();
 }
 

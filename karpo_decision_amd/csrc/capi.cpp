@@ -170,9 +170,9 @@ extern "C" int karpo_attn_fwd(const KarpoAttnArgs* a, void* stream) {
   const int32_t* plan = a->plan;
   if (plan == nullptr) {
     int32_t* dplan = reinterpret_cast<int32_t*>(ws);
-    if (launch_plan(a->q_cu, a->k_cu, a->n_seq, g, a->window_left, a->window_right, dplan, (int)z.tiles,
-                    (int)z.merges, (int)z.items, dplan + z.plan_entries, s) != hipSuccess)
-      return KARPO_ATTN_ERR_LAUNCH;
+    const PlanJob job = {a->q_cu, a->k_cu, g, a->window_left, a->window_right, dplan, (int)z.tiles, (int)z.merges,
+                         (int)z.items, dplan + z.plan_entries};
+    if (launch_plan(&job, 1, a->n_seq, s) != hipSuccess) return KARPO_ATTN_ERR_LAUNCH;
     plan = dplan;
   }
 
@@ -281,7 +281,7 @@ BwdSizes bwd_sizes_of(const KarpoAttnBwdArgs* b) {
   z.stats_bytes = ((int64_t)a->heads * 2 * a->total_q * 4 + 255) / 256 * 256;
   z.plan_q = 0;
   z.plan_k = kPlanHeader + kItemInts * z.tiles_q;
-  const int64_t ints = z.plan_k + kPlanHeader + kItemInts * z.tiles_k + a->n_seq + 1;
+  const int64_t ints = z.plan_k + kPlanHeader + kItemInts * z.tiles_k + 2 * ((int64_t)a->n_seq + 1);  // 2 tile bases
   z.bytes = z.stats_bytes + (ints * 4 + 255) / 256 * 256;
   return z;
 }
@@ -385,8 +385,9 @@ extern "C" int karpo_attn_bwd(const KarpoAttnBwdArgs* b, void* stream) {
   p.right = a->window_right;
   p.c = a->scale * 1.4426950408889634f;
   p.scale = a->scale;
+  int32_t* const tile_base = ints + z.plan_k + kPlanHeader + kItemInts * z.tiles_k;
   if (launch_bwd(p, a->head_dim, gq, gk, ints + z.plan_q, ints + z.plan_k, z.tiles_q, z.tiles_k, (int)z.tiles_q, 0,
-                 (int)z.tiles_k, 0, ints + z.plan_k + kPlanHeader + kItemInts * z.tiles_k, a->n_seq,
+                 (int)z.tiles_k, 0, tile_base, tile_base + a->n_seq + 1, a->n_seq,
                  static_cast<hipStream_t>(stream)) != hipSuccess)
     return KARPO_ATTN_ERR_LAUNCH;
   return KARPO_ATTN_OK;

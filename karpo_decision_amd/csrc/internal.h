@@ -72,7 +72,7 @@ hipError_t launch_bwd_pair(const BwdParams& p, const Geometry& gq, const Geometr
                            int32_t* plan_k, int64_t items_q, int64_t items_k, hipStream_t stream);
 hipError_t launch_bwd(const BwdParams& p, int head_dim, const Geometry& gq, const Geometry& gk, int32_t* plan_q,
                       int32_t* plan_k, int64_t items_q, int64_t items_k, int tiles_q, int merges_q, int tiles_k,
-                      int merges_k, int32_t* tile_base, int n_seq, hipStream_t stream);
+                      int merges_k, int32_t* tile_base_q, int32_t* tile_base_k, int n_seq, hipStream_t stream);
 
 // karpo_attn_norm_rope's kernel.
 struct NormRopeParams {
@@ -92,9 +92,18 @@ hipError_t launch_norm_rope(const NormRopeParams& p, int head_dim, hipStream_t s
 hipError_t launch_forward(const Params& p, int head_dim, const Geometry& g, int64_t items, int64_t merges,
                           hipStream_t stream);
 
-// The device planner: writes the work list for the bounds into `plan` (room for `merges` split tiles and `items`
-// items; at most `tiles` tiles are planned) using `tile_base` (n_seq + 1 ints) as scratch.
-hipError_t launch_plan(const int32_t* q_cu, const int32_t* k_cu, int n_seq, const Geometry& g, int left, int right,
-                       int32_t* plan, int tiles, int merges, int items, int32_t* tile_base, hipStream_t stream);
+// One work list for the device planner: from the bounds into `plan` (room for `merges` split tiles and `items`
+// items; at most `tiles` tiles are planned), with `tile_base` (n_seq + 1 ints) as its scratch.
+struct PlanJob {
+  const int32_t* q_cu;
+  const int32_t* k_cu;
+  Geometry g;
+  int left, right;
+  int32_t* plan;
+  int tiles, merges, items;
+  int32_t* tile_base;
+};
+// The device planner: one workgroup per job (one or two), one launch.
+hipError_t launch_plan(const PlanJob* jobs, int n_jobs, int n_seq, hipStream_t stream);
 
 }  // namespace karpo
