@@ -208,6 +208,30 @@ def test_branched_varlen_with_an_empty_sequence(gpu, heads, kv_heads, head, caus
     assert_close(got, want, f"branched causal={causal}")
 
 
+@pytest.mark.parametrize("heads,kv_heads,head,shapes", [(32, 16, 128, {1400: 2, 5000: 0, 70000: 3}),
+                                                       (12, 4, 128, {1400: 2, 5000: 0, 70000: 3}),
+                                                       (16, 8, 256, {1400: 2, 9000: 0})])
+@pytest.mark.parametrize("left", [-1, 200])
+def test_every_tile_shape_matches_the_oracle(gpu, heads, kv_heads, head, shapes, left):
+    """max_q is an upper bound of the query runs that selects the tile shape (small, wide, long; the narrow shape has
+    its own tests): one pack run under each shape its max_q values select, each against the oracle."""
+    torch.manual_seed(5)
+    lengths = [1400, 513, 1, 700]
+    cu = _lengths_cu(lengths)
+    n = cu[-1]
+    q = (torch.randn(n, heads, head, device=gpu) / 4).bfloat16()
+    k = (torch.randn(n, kv_heads, head, device=gpu) / 4).bfloat16()
+    v = torch.randn(n, kv_heads, head, device=gpu).bfloat16()
+    cu_t = torch.tensor(cu, dtype=torch.int32, device=gpu)
+    scale = 1 / math.sqrt(head)
+    want = oa.packed_attention(q.cpu(), k.cpu(), v.cpu(), cu, cu, scale, left, 0)
+    for max_q, shape in shapes.items():
+        assert _lib.kernel_shape(heads, kv_heads, head, max_q) == shape
+        with torch.inference_mode():
+            got = ops.run(q, k, v, cu_t, cu_t, max_q, scale, window_left=left, window_right=0)
+        assert_close(got, want, f"shape {shape} (max_q {max_q}, D={head}, left={left})")
+
+
 def test_keys_past_32_bit_offsets(gpu):
     """Key rows of 16 heads x 128 = 2,048 elements: row 2^20 starts at element 2^31. A first sequence holds 2^20
     keys and no queries, a second 64 queries over the 300 keys after them (tests/gpu/test_triton_attention.py:93-104)."""
