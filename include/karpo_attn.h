@@ -194,7 +194,9 @@ int karpo_attn_plan(const KarpoAttnArgs* args, const int32_t* q_cu_host, const i
                     int32_t* plan, int64_t capacity);
 
 /* Query rows per tile, keys per step and query heads per work item the kernel uses for these heads / head size and
- * the longest query run max_q (packs whose sequences fit one wave's 32 query vectors take one-wave tiles). */
+ * the longest query run max_q: packs whose sequences fit one wave's 32 query vectors take one-wave tiles; runs up to
+ * 4,096 queries at head size 128 (8,192 at 256) take 4-wave tiles; longer ones the wide tiles (12 waves at 128, 32
+ * keys per step; 64 keys per step above 65,536 queries). */
 int karpo_attn_tile_shape(int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t max_q, int32_t* rows_per_tile,
                           int32_t* keys_per_step, int32_t* heads_per_item);
 
