@@ -236,7 +236,17 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
   __shared__ __attribute__((aligned(1024))) char k_lds1[TILE];
   __shared__ __attribute__((aligned(1024))) char v_lds0[TILE];
   __shared__ __attribute__((aligned(1024))) char v_lds1[TILE];
-  __shared__ int red[2][W];  // the workgroup's key envelope (unused, so not allocated, by one-wave workgroups)
+  // a pair's exchange of partial S^T: 16 floats per lane and wave (32 KiB for the 8-wave tile, so the tile's LDS is
+  // exactly 160 KiB)
+  __shared__ __attribute__((aligned(16))) f32x4 xch[PAIR ? W : 1][PAIR ? 4 * 64 : 1];
+  // the workgroup's key envelope (unused, so not allocated, by one-wave workgroups; in the exchange slots for pairs,
+  // read by every wave before the barrier that precedes the first exchange)
+  __shared__ int red_s[PAIR ? 1 : 2][PAIR ? 1 : W];
+  int(*red)[W];
+  if constexpr (PAIR)
+    red = (int(*)[W])&xch[0][0];
+  else
+    red = red_s;
 
   // a plan made for another tile shape is not run (its rows stay unwritten)
   if (p.plan[2] != BN || p.plan[5] != W) return;
@@ -473,12 +483,11 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
       }
     }
     if constexpr (PAIR) {
-      // the pair adds its two partial S^T through LDS: each wave's 16 floats per lane go to its 4 KiB slot of this
-      // step's K tile, which every wave has finished reading at the first barrier (all waves pass both barriers)
-      static_assert(KB == 1 && W * 4096 <= TILE, "one 32-key block per step; the slots fit the K tile");
-      KA_LDS f32x4* slot = (KA_LDS f32x4*)(const_cast<KA_LDS char*>(kt) + wave * 4096) + lane;
-      const KA_LDS f32x4* other = (const KA_LDS f32x4*)(kt + (wave ^ 1) * 4096) + lane;
-      __syncthreads();
+      // the pair adds its two partial S^T through LDS: each wave's 16 floats per lane go to its 4 KiB exchange slot
+      // (read by the partner after the barrier; written again only after the step's end barrier)
+      static_assert(KB == 1, "one 32-key block per step");
+      KA_LDS f32x4* slot = (KA_LDS f32x4*)&xch[wave][0] + lane;
+      const KA_LDS f32x4* other = (const KA_LDS f32x4*)&xch[wave ^ 1][0] + lane;
       if (active) {
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4)
