@@ -16,11 +16,10 @@
 //     the query rows that see the tile streamed in steps of 32 rows of one head (every head of the GQA group in turn,
 //     which sums the group's gradients): S = Q K^T and dP = dO V^T with Q and dO as row operands, dV^T += dO^T P and
 //     dK^T += Q^T dS with Q and dO read transposed from the same tiles (S layout; a dV-only launch stages dO in the
-//     transposed-read layout, whose copies read whole rows). One launch computes both
-//     (MODE 3), or two launches compute dV (MODE 1) and dK (MODE 2), each recomputing S: always at head size 256
-//     (both accumulators and both operands do not fit one wave's registers), and at 128 for packs with many key tiles
-//     (two or three waves per SIMD instead of one overlap each other's softmax and MFMA work; a small pack has too
-//     few tiles to fill the GPU twice).
+//     transposed-read layout, whose copies read whole rows). One launch computes both (MODE 3; at head size 256 one
+//     wave per SIMD holds both accumulators in 256 AGPRs), or, at head size 128 for packs with many key tiles, two
+//     launches compute dV (MODE 1) and dK (MODE 2), each recomputing S (two or three waves per SIMD instead of one
+//     overlap each other's softmax and MFMA work; a small pack has too few tiles to fill the GPU twice).
 // Both streams advance their copy addresses by pointer increments per step (no per-step address recomputation: the
 // scalar unit is shared by the CU's waves and a step is short).
 // Rows of a product's row operand are fed in the order that swaps bits 2 and 3 of the row index (key_row), so each
@@ -45,7 +44,7 @@ constexpr int64_t kSplitKeyTiles = 8 * kComputeUnits;
 template <int D> struct BwdCfg {
   static constexpr int OCC_Q = D >= 256 ? 1 : 2;  // waves per SIMD the registers are budgeted for
   static constexpr int BLOCKS_Q = OCC_Q * 4 / bwd_q_waves(D) > 0 ? OCC_Q * 4 / bwd_q_waves(D) : 1;
-  template <int MODE> static constexpr int occ_k() { return MODE == 3 || D >= 256 ? 1 : MODE == 1 ? 3 : 2; }
+  template <int MODE> static constexpr int occ_k() { return MODE == 3 ? 1 : MODE == 1 ? 3 : 2; }
 };
 
 // Row (within a 32-row step) of result register j of a lane in half `half` (row operands fed in key_row order).
@@ -632,12 +631,12 @@ static hipError_t launch_bwd_d(const BwdParams& p, const Geometry& gq, const Geo
   pk.n_hg = gk.n_hg;
   const dim3 grid((unsigned)(items_k * gk.n_hg));
   if (items_k > 0) {
-    if (D >= 256 || (D == 128 && items_k * gk.n_hg >= kSplitKeyTiles)) {
-      if constexpr (D >= 128) {
+    if (D == 128 && items_k * gk.n_hg >= kSplitKeyTiles) {
+      if constexpr (D == 128) {
         hipLaunchKernelGGL((bwd_dkdv_kernel<D, 1>), grid, dim3(64 * kBwdWaves), 0, stream, pk);
         hipLaunchKernelGGL((bwd_dkdv_kernel<D, 2>), grid, dim3(64 * kBwdWaves), 0, stream, pk);
       }
-    } else if constexpr (D <= 128) {
+    } else {
       hipLaunchKernelGGL((bwd_dkdv_kernel<D, 3>), grid, dim3(64 * kBwdWaves), 0, stream, pk);
     }
   }
