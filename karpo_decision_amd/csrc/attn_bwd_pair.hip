@@ -3,7 +3,7 @@
 // cannot hold a 512-wide operand row and accumulator row for 32 vectors (128 + 256 registers per lane for each), so
 // each wave of a pair holds half of D: half of the operands in registers and half of the gradient accumulators. A
 // step's S (and dP) is a sum over all of D: each wave computes the product over its half and the pair adds the two
-// partials through LDS (low half + high half, in that order, so the sums are bit-equal wherever they are formed).
+// partials through LDS (a sum of two terms, bit-equal in either order, so the sums agree wherever they are formed).
 //
 // dQ kernel: both waves of a pair add the whole step's partials and run the same softmax; two barriers per step, (1)
 // after the S / dP products (the partials are written), (2) at its end. K, read as rows and transposed (S layout),
@@ -47,24 +47,17 @@ __device__ __forceinline__ void exchange_write(KA_LDS f32x4* slot, int lane, con
     if (with_b) slot[(q4 + 4) * 64 + lane] = f32x4{b[4 * q4], b[4 * q4 + 1], b[4 * q4 + 2], b[4 * q4 + 3]};
   }
 }
-// Adds the partner's partials: low half (wave dh = 0) + high half, in that order in both waves.
-__device__ __forceinline__ void exchange_add(const KA_LDS f32x4* other, int lane, int dh, f32x16& a, f32x16& b,
-                                             bool with_b) {
+// Adds the partner's partials (a sum of two terms: bit-equal in both waves, addition commutes exactly).
+__device__ __forceinline__ void exchange_add(const KA_LDS f32x4* other, int lane, f32x16& a, f32x16& b, bool with_b) {
 #pragma unroll
   for (int q4 = 0; q4 < 4; ++q4) {
     const f32x4 o = other[q4 * 64 + lane];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float mine = a[4 * q4 + e];
-      a[4 * q4 + e] = dh ? o[e] + mine : mine + o[e];
-    }
+    for (int e = 0; e < 4; ++e) a[4 * q4 + e] += o[e];
     if (with_b) {
       const f32x4 ob = other[(q4 + 4) * 64 + lane];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float mine = b[4 * q4 + e];
-        b[4 * q4 + e] = dh ? ob[e] + mine : mine + ob[e];
-      }
+      for (int e = 0; e < 4; ++e) b[4 * q4 + e] += ob[e];
     }
   }
 }
@@ -204,7 +197,7 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void bwd_dq_pair_kernel(BwdPara
     __syncthreads();  // 1: V is read and the partials written
     if (ahead) copy_v();
     if (act) {
-      exchange_add(other, lane, dh, st, dpt, true);
+      exchange_add(other, lane, st, dpt, true);
       float x[KC][8];
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc)
@@ -269,7 +262,7 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void bwd_dq_pair_kernel(BwdPara
 // ---- dK and dV: key tiles of two pairs (64 keys), 32 query rows of one head per step, each head of the GQA group in
 // turn, rows from the last step down (as attn_bwd.hip's key-stationary kernel). A wave holds half of D of both
 // accumulators (2 x 128 registers) and of K and V. The pair splits a step's softmax by row block: wave dh computes P
-// and dS of rows dh*16 .. +16 from the partner's partial S and dP of those rows (low half + high half), and the two
+// and dS of rows dh*16 .. +16 from its own and the partner's partial S and dP of those rows, and the two
 // swap their P and dS (bf16, the MFMA operands) through LDS: 24 KiB of exchange instead of 32, so Q and dO (read as
 // rows and transposed) both get two buffers.
 template <int D>
@@ -417,33 +410,41 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void bwd_dkdv_pair_kernel(BwdPa
         const bf16x8 o = *(const KA_LDS bf16x8*)(ot + at);
         dpt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(o, vop[dc], dpt, 0, 0, 0);
       }
-      // registers 8 kc .. 8 kc + 7 hold rows kc*16 + half*8 .. +8: the partner's block (kc = 1 - dh) to it
-      f32x4 w0, w1, w2, w3;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        w0[e] = dh ? st[e] : st[8 + e];
-        w1[e] = dh ? st[4 + e] : st[12 + e];
-        w2[e] = dh ? dpt[e] : dpt[8 + e];
-        w3[e] = dh ? dpt[4 + e] : dpt[12 + e];
+      // registers 8 kc .. 8 kc + 7 hold rows kc*16 + half*8 .. +8: the partner's block (kc = 1 - dh) to it (a
+      // wave-uniform branch, so each wave moves only the 16 registers it sends)
+      if (dh) {
+        mine[lane] = f32x4{st[0], st[1], st[2], st[3]};
+        mine[64 + lane] = f32x4{st[4], st[5], st[6], st[7]};
+        mine[128 + lane] = f32x4{dpt[0], dpt[1], dpt[2], dpt[3]};
+        mine[192 + lane] = f32x4{dpt[4], dpt[5], dpt[6], dpt[7]};
+      } else {
+        mine[lane] = f32x4{st[8], st[9], st[10], st[11]};
+        mine[64 + lane] = f32x4{st[12], st[13], st[14], st[15]};
+        mine[128 + lane] = f32x4{dpt[8], dpt[9], dpt[10], dpt[11]};
+        mine[192 + lane] = f32x4{dpt[12], dpt[13], dpt[14], dpt[15]};
       }
-      mine[lane] = w0;
-      mine[64 + lane] = w1;
-      mine[128 + lane] = w2;
-      mine[192 + lane] = w3;
     }
     __syncthreads();  // 1: the partials are written
     bf16x8 pm, dm;
-    if (act) {  // this wave's block: S and dP summed low half + high half, P and dS of rows r0 + dh*16 + half*8 + t
+    if (act) {  // this wave's block: S and dP summed over D, P and dS of rows r0 + dh*16 + half*8 + t
       const f32x4 x0 = other[lane], x1 = other[64 + lane], x2 = other[128 + lane], x3 = other[192 + lane];
-      float sv[8], pv[8];
+      float sv[8], pv[8];  // a sum of two terms (bit-equal in either order)
+      if (dh) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float s0 = dh ? st[8 + e] : st[e], s1 = dh ? st[12 + e] : st[4 + e];
-        const float p0 = dh ? dpt[8 + e] : dpt[e], p1 = dh ? dpt[12 + e] : dpt[4 + e];
-        sv[e] = dh ? x0[e] + s0 : s0 + x0[e];
-        sv[4 + e] = dh ? x1[e] + s1 : s1 + x1[e];
-        pv[e] = dh ? x2[e] + p0 : p0 + x2[e];
-        pv[4 + e] = dh ? x3[e] + p1 : p1 + x3[e];
+        for (int e = 0; e < 4; ++e) {
+          sv[e] = st[8 + e] + x0[e];
+          sv[4 + e] = st[12 + e] + x1[e];
+          pv[e] = dpt[8 + e] + x2[e];
+          pv[4 + e] = dpt[12 + e] + x3[e];
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          sv[e] = st[e] + x0[e];
+          sv[4 + e] = st[4 + e] + x1[e];
+          pv[e] = dpt[e] + x2[e];
+          pv[4 + e] = dpt[4 + e] + x3[e];
+        }
       }
       const KA_LDS float* rs = tst + dh * 16 + half * 8;
       const f32x4 l0 = *(const KA_LDS f32x4*)rs, l1 = *(const KA_LDS f32x4*)(rs + 4);
@@ -476,12 +477,16 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void bwd_dkdv_pair_kernel(BwdPa
     if (act) {
       const bf16x8 po = pother[lane], dso = pother[64 + lane];
       bf16x8 pb[KC], dsb[KC];
-#pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        pb[0][t] = dh ? po[t] : pm[t];
-        pb[1][t] = dh ? pm[t] : po[t];
-        dsb[0][t] = dh ? dso[t] : dm[t];
-        dsb[1][t] = dh ? dm[t] : dso[t];
+      if (dh) {
+        pb[0] = po;
+        pb[1] = pm;
+        dsb[0] = dso;
+        dsb[1] = dm;
+      } else {
+        pb[0] = pm;
+        pb[1] = po;
+        dsb[0] = dm;
+        dsb[1] = dso;
       }
       // dV^T += dO^T P and dK^T += Q^T dS, this wave's half of D, dO and Q read transposed
 #pragma unroll

@@ -496,16 +496,12 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
       __syncthreads();
       if (active) {
 #pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {  // low half + high half in that order in both waves: equal sums
+        for (int q4 = 0; q4 < 4; ++q4) {  // a sum of two terms: equal in both waves (addition commutes exactly)
           const f32x4 o = other[q4 * 64];
-          const float x0 = dh ? o.x : st[0][4 * q4], y0 = dh ? st[0][4 * q4] : o.x;
-          const float x1 = dh ? o.y : st[0][4 * q4 + 1], y1 = dh ? st[0][4 * q4 + 1] : o.y;
-          const float x2 = dh ? o.z : st[0][4 * q4 + 2], y2 = dh ? st[0][4 * q4 + 2] : o.z;
-          const float x3 = dh ? o.w : st[0][4 * q4 + 3], y3 = dh ? st[0][4 * q4 + 3] : o.w;
-          st[0][4 * q4] = x0 + y0;
-          st[0][4 * q4 + 1] = x1 + y1;
-          st[0][4 * q4 + 2] = x2 + y2;
-          st[0][4 * q4 + 3] = x3 + y3;
+          st[0][4 * q4] += o.x;
+          st[0][4 * q4 + 1] += o.y;
+          st[0][4 * q4 + 2] += o.z;
+          st[0][4 * q4 + 3] += o.w;
         }
       }
     }
