@@ -445,7 +445,7 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::template occ_k<MODE>()) 
   const uint16_t* c_q = p.q + (int64_t)(qa + r_last) * p.sq_t + (int64_t)h0 * p.sq_h;
   const uint16_t* c_o = p.dout + (int64_t)(qa + r_last) * p.sdo_t + (int64_t)h0 * p.sdo_h;
   const float* c_st = p.stats + (int64_t)h0 * 2 * p.total_q + qa + r_last;
-  auto copy_step = [&](int s, KA_LDS char* tqk, KA_LDS char* tok, KA_LDS float* tst) {
+  auto copy_step = [&](KA_LDS char* tqk, KA_LDS char* tok, KA_LDS float* tst) {
     const int rows = min(lq - c_r0, BQ);
     const uint16_t* qs = c_q;
     const uint16_t* os = c_o;
@@ -494,13 +494,13 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::template occ_k<MODE>()) 
   KA_LDS float* const tst0 = (KA_LDS float*)sts0;
   KA_LDS float* const tst1 = (KA_LDS float*)sts1;
   int r_cur = r_last;
-  if (n_steps > 0) copy_step(0, tqk0, tok0, tst0);
+  if (n_steps > 0) copy_step(tqk0, tok0, tst0);
   wait_vmcnt<0>();
   __syncthreads();
 
   auto step = [&](int s, const KA_LDS char* tqk, const KA_LDS char* tok, const KA_LDS float* tst, KA_LDS char* nqk,
                   KA_LDS char* nok, KA_LDS float* nst) {
-    if (s + 1 < n_steps) copy_step(s + 1, nqk, nok, nst);
+    if (s + 1 < n_steps) copy_step(nqk, nok, nst);
     const int r0 = r_cur;
     r_cur = r_cur == r_first ? r_last : r_cur - BQ;
     if (r0 < whi && r0 + BQ > wlo) {

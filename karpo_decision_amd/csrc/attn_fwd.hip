@@ -72,6 +72,10 @@ __device__ __forceinline__ float sigmoid(float g) { return 1.f / (1.f + __expf(-
 // every address is clamped in bounds and selects discard what does not apply, so the loads of a group of chunks
 // issue together (one memory latency per group, not per chunk). Without a weight the host points q_norm_w at
 // readable memory; the weight factor is wm * weight[d] + wa (WEIGHT: 1, 0; ONE_PLUS: 1, 1; PLAIN: 0, 1).
+template <int DC, int RC>
+__device__ __forceinline__ void query_prologue_regs(const Params& p, int64_t qrow, int half, float r, float wm,
+                                                    float wa, bool norm, u32x4 (&x)[DC]);
+
 template <int D, int NC>
 __device__ __forceinline__ void query_prologue(const Params& p, const uint16_t* row, int64_t qrow, int half, int c0,
                                                u32x4 (&x)[NC]) {
@@ -199,8 +203,7 @@ __device__ __forceinline__ void query_prologue_regs(const Params& p, int64_t qro
 }
 
 // Four output elements of one query: bf16(o), then the gate's bf16(bf16(o) * sigmoid(g)) when there is one.
-__device__ __forceinline__ u32x2 output4(const Params& p, float o0, float o1, float o2, float o3,
-                                         const uint16_t* gate4) {
+__device__ __forceinline__ u32x2 output4(float o0, float o1, float o2, float o3, const uint16_t* gate4) {
   if (gate4 != nullptr) {
     const u32x2 g = *(const u32x2*)gate4;
     const u32x4 gv = {g[0], g[1], 0, 0};
@@ -605,7 +608,7 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
         *(u32x2*)(op + db * 32 + g4 * 8) =
-            output4(p, acc[db][g4 * 4] * inv, acc[db][g4 * 4 + 1] * inv, acc[db][g4 * 4 + 2] * inv,
+            output4(acc[db][g4 * 4] * inv, acc[db][g4 * 4 + 1] * inv, acc[db][g4 * 4 + 2] * inv,
                     acc[db][g4 * 4 + 3] * inv, gp != nullptr ? gp + db * 32 + g4 * 8 : nullptr);
       }
     }
@@ -664,7 +667,7 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(Params p) {
     const uint16_t* gp =
         p.gate != nullptr ? p.gate + (int64_t)(qa + pos) * p.sg_t + (int64_t)head * p.sg_h + d : nullptr;
     *(u32x2*)(p.o + (int64_t)(qa + pos) * p.so_t + (int64_t)head * p.so_h + d) =
-        output4(p, num.x * inv, num.y * inv, num.z * inv, num.w * inv, gp);
+        output4(num.x * inv, num.y * inv, num.z * inv, num.w * inv, gp);
   }
 }
 
