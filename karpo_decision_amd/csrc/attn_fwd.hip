@@ -234,11 +234,26 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
   constexpr int INSTS = (BLKS + W - 1) / W;       // per wave (the last waves may issue fewer)
   static_assert(BLKS >= 1, "a tile holds at least one DMA instruction");
 
+  // K/V buffers: NB - 1 steps of copies in flight. One-wave tiles that stream their keys (decode-shaped packs, HBM
+  // bound) keep three steps in flight in 64 KiB (two workgroups per CU: 96 KiB of copies in flight per CU instead of
+  // five workgroups' 80; the markers layer's attention kernel 115.9 -> 109.6 us, planned two per CU either way); the
+  // others two buffers. The deeper ring counts its own copies to wait for one step's, so it is only built where every
+  // copy instruction is issued unconditionally (one wave, no row table).
+  constexpr int NB = SHAPE == kNarrow && W == 1 && !GATHER && D <= 128 ? 4 : 2;
+  static_assert(NB == 2 || (W == 1 && BLKS == INSTS), "the ring waits on a fixed count of its wave's copies");
+  constexpr int CPS = 2 * INSTS;  // copy instructions per step of a one-wave tile (K and V)
+  static_assert(NB == 2 || (NB - 2) * CPS <= 63, "vmcnt counts at most 63 outstanding operations");
   // separate arrays per buffer: the compiler then sees that a step's copy never writes the tiles it reads
   __shared__ __attribute__((aligned(1024))) char k_lds0[TILE];
   __shared__ __attribute__((aligned(1024))) char k_lds1[TILE];
   __shared__ __attribute__((aligned(1024))) char v_lds0[TILE];
   __shared__ __attribute__((aligned(1024))) char v_lds1[TILE];
+  __shared__ __attribute__((aligned(1024))) char k_lds2[NB > 2 ? TILE : 16];
+  __shared__ __attribute__((aligned(1024))) char v_lds2[NB > 2 ? TILE : 16];
+  __shared__ __attribute__((aligned(1024))) char k_lds3[NB > 3 ? TILE : 16];
+  __shared__ __attribute__((aligned(1024))) char v_lds3[NB > 3 ? TILE : 16];
+  __shared__ __attribute__((aligned(1024))) char k_lds4[NB > 4 ? TILE : 16];
+  __shared__ __attribute__((aligned(1024))) char v_lds4[NB > 4 ? TILE : 16];
   // a pair's exchange of partial S^T: 16 floats per lane and wave (32 KiB for the 8-wave tile, so the tile's LDS is
   // exactly 160 KiB)
   __shared__ __attribute__((aligned(16))) f32x4 xch[PAIR ? W : 1][PAIR ? 4 * 64 : 1];
@@ -451,25 +466,68 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
   const float c = p.c;
   const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
 
+  // buffer i of the ring (i a constant once the loops below unroll; a two-buffer kernel never names the others, so
+  // they are not allocated)
+  auto kbuf = [&](int i) -> KA_LDS char* {
+    if constexpr (NB > 2) {
+      switch (i) {
+        case 2: return (KA_LDS char*)k_lds2;
+        case 3: return (KA_LDS char*)k_lds3;
+        case 4: return (KA_LDS char*)k_lds4;
+        default: break;
+      }
+    }
+    return i == 0 ? (KA_LDS char*)k_lds0 : (KA_LDS char*)k_lds1;
+  };
+  auto vbuf = [&](int i) -> KA_LDS char* {
+    if constexpr (NB > 2) {
+      switch (i) {
+        case 2: return (KA_LDS char*)v_lds2;
+        case 3: return (KA_LDS char*)v_lds3;
+        case 4: return (KA_LDS char*)v_lds4;
+        default: break;
+      }
+    }
+    return i == 0 ? (KA_LDS char*)v_lds0 : (KA_LDS char*)v_lds1;
+  };
+  // waits until the copies of step s + 1 have landed, given that the ones of steps up to s + NB - 1 were issued
+  // after them (the ring: exactly CPS instructions per issued step)
+  auto wait_next = [&](int s) {
+    if constexpr (NB == 2) {
+      wait_vmcnt<0>();
+    } else {
+      const int later = min(NB - 2, n_steps - 2 - s);  // steps issued after step s + 1
+      if (later >= 3) wait_vmcnt<3 * CPS>();
+      else if (later == 2) wait_vmcnt<2 * CPS>();
+      else if (later == 1) wait_vmcnt<CPS>();
+      else wait_vmcnt<0>();
+    }
+  };
   KA_LDS char* const kt0 = (KA_LDS char*)k_lds0;
   KA_LDS char* const kt1 = (KA_LDS char*)k_lds1;
   KA_LDS char* const vt0 = (KA_LDS char*)v_lds0;
   KA_LDS char* const vt1 = (KA_LDS char*)v_lds1;
-  // prologue: the first step in flight (and the second's table rows), wait for it
-  if (n_steps > 0) {
-    fetch_rows(j_first);
-    copy_step(j_first, kt0, vt0);
-    if (n_steps > 1) fetch_rows(j_first + BN);
+  // prologue: the first NB - 1 steps in flight (and the next one's table rows), wait for the first
+  if constexpr (NB == 2) {
+    if (n_steps > 0) {
+      fetch_rows(j_first);
+      copy_step(j_first, kt0, vt0);
+      if (n_steps > 1) fetch_rows(j_first + BN);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < NB - 1; ++i)
+      if (i < n_steps) copy_step(j_first + i * BN, kbuf(i), vbuf(i));
   }
   if constexpr (!PAIR) load_q();
-  wait_vmcnt<0>();
+  wait_next(-1);
   __syncthreads();
 
-  // step s: copy step s + 1 into (kn, vn) while computing on (kt, vt); then wait for that copy
+  // step s: copy step s + NB - 1 into (kn, vn) while computing on (kt, vt); then wait for step s + 1's copy
   auto step = [&](int s, const KA_LDS char* kt, const KA_LDS char* vt, KA_LDS char* kn, KA_LDS char* vn) {
     const int j0 = j_first + s * BN;
-    if (s + 1 < n_steps) copy_step(j0 + BN, kn, vn);
-    if (GATHER && s + 2 < n_steps) fetch_rows(j0 + 2 * BN);
+    if (s + NB - 1 < n_steps) copy_step(j0 + (NB - 1) * BN, kn, vn);
+    if (GATHER && s + NB < n_steps) fetch_rows(j0 + NB * BN);
     const bool active = j0 < whi && j0 + BN > wlo;  // wave-uniform: some query of this wave sees a key of the step
     if (PAIR || active) {  // a pair enters together (its barriers), each wave computes only when active
     f32x16 st[KB];
@@ -566,15 +624,26 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
       }
     }
     }
-    wait_vmcnt<0>();
+    wait_next(s);
     __syncthreads();
   };
   int s = 0;
-  for (; s + 1 < n_steps; s += 2) {
-    step(s, kt0, vt0, kt1, vt1);
-    step(s + 1, kt1, vt1, kt0, vt0);
+  if constexpr (NB == 2) {
+    for (; s + 1 < n_steps; s += 2) {
+      step(s, kt0, vt0, kt1, vt1);
+      step(s + 1, kt1, vt1, kt0, vt0);
+    }
+    if (s < n_steps) step(s, kt0, vt0, kt1, vt1);
+  } else {  // the ring unrolled NB times: step s computes on buffer s % NB and copies into (s + NB - 1) % NB
+    for (; s + NB - 1 < n_steps; s += NB) {
+#pragma unroll
+      for (int i = 0; i < NB; ++i)
+        step(s + i, kbuf(i), vbuf(i), kbuf((i + NB - 1) % NB), vbuf((i + NB - 1) % NB));
+    }
+#pragma unroll
+    for (int i = 0; i < NB - 1; ++i)
+      if (s + i < n_steps) step(s + i, kbuf(i), vbuf(i), kbuf((i + NB - 1) % NB), vbuf((i + NB - 1) % NB));
   }
-  if (s < n_steps) step(s, kt0, vt0, kt1, vt1);
 
   // ---- store: lane (col, half) holds d = db*32 + (j/4)*8 + half*4 + j%4 of its query vector
   const float lt = half_swap_sum(l);

@@ -49,12 +49,13 @@ KA_HD constexpr int tile_vectors(int head_dim, int shape) {
 KA_HD constexpr int tile_keys(int head_dim, int shape) {
   return head_dim == 64 ? 64 : head_dim >= 256 ? 32 : shape == kLong ? 64 : 32;
 }
-// Workgroups per CU the split policy plans for (its concurrency): the resident ones (two K and two V tiles of
+// Workgroups per CU the split policy plans for (its concurrency): the resident ones (the K and V buffers of
 // tile_keys x head_dim bf16 per workgroup in 160 KiB of LDS, and the registers), except small tiles, planned one per CU
 // although two or three run there: splitting to the per-workgroup share made more split parts than their merge repays
-// (Qwen pack 0.110 against 0.097 ms).
+// (Qwen pack 0.110 against 0.097 ms). One-wave tiles at head_dim 64 / 128 are two per CU (a ring of four K/V buffers;
+// with the row table two buffers, five resident, planned two per CU all the same: the markers layer's merge halves).
 KA_HD constexpr int tiles_per_cu(int head_dim, int shape) {
-  return shape == kNarrow ? (head_dim == 512 ? 1 : head_dim == 256 ? 2 : 5) : head_dim == 64 ? 4 : 1;
+  return shape == kNarrow ? (head_dim == 512 ? 1 : 2) : head_dim == 64 ? 4 : 1;
 }
 constexpr int kComputeUnits = 256;   // MI355X
 constexpr int kPlanHeader = 8;       // int32 header of a plan (see karpo_attn.h)

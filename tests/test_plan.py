@@ -61,8 +61,9 @@ def host_plan(q_cu, k_cu, heads, kv_heads, head_dim, left, right, max_q=_lib.LON
 
 
 #: Workgroups per CU the split policy plans for, per (head_dim, one-wave tiles): the register and LDS budgets of the
-#: kernels (small tiles, 4 waves at head_dim 128 / 256, are planned one per CU like the wide ones).
-TILES_PER_CU = {(64, False): 4, (128, False): 1, (256, False): 1, (512, False): 1, (64, True): 5, (128, True): 5,
+#: kernels (small tiles, 4 waves at head_dim 128 / 256, are planned one per CU like the wide ones; one-wave tiles at
+#: 64 / 128 two per CU, their ring of four K/V buffers).
+TILES_PER_CU = {(64, False): 4, (128, False): 1, (256, False): 1, (512, False): 1, (64, True): 2, (128, True): 2,
                 (256, True): 2, (512, True): 1}
 GEOMETRIES = [(8, 2, 64), (16, 8, 128), (32, 16, 128), (16, 8, 256), (12, 4, 128), (10, 2, 128), (4, 4, 64),
               (32, 4, 512), (6, 2, 512)]
@@ -130,9 +131,9 @@ def test_markers_plan_splits_keys():
     q_cu = [0, 1, 2]
     header, merges, items = host_plan(q_cu, k_cu, 32, 16, 128, -1, -1, 1)
     assert header[1:4] == [16, 32, 2] and header[5] == 1
-    # 1024 + 226 steps of 32 keys x 16 head groups over 5 x 256 one-wave workgroups: parts of 16 steps
-    assert merges == [(0, 0, 64, 0), (1, 0, 15, 64)]
-    assert len(items) == 79 and header[7] == 79
+    # 1024 + 226 steps of 32 keys x 16 head groups over 2 x 256 one-wave workgroups: parts of at most 40 steps
+    assert merges == [(0, 0, 26, 0), (1, 0, 6, 26)]
+    assert len(items) == 32 and header[7] == 32
 
 
 def test_tile_geometry():
