@@ -131,8 +131,7 @@ def _args(query: Tensor, key: Tensor, value: Tensor, out: Tensor | None, q_cu: T
     return a
 
 
-@torch.library.custom_op(f"{NAMESPACE}::packed_attention", mutates_args=())
-def packed_attention(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_cu: Tensor, max_q: int,
+def _packed_attention(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_cu: Tensor, max_q: int,
                      scale: float, window_left: int, window_right: int, spans: Tensor | None,
                      plan: Tensor | None, plan_split_tiles: int = -1, key_rows: Tensor | None = None,
                      q_norm: int = 0, q_norm_eps: float = 0.0, q_norm_weight: Tensor | None = None,
@@ -189,6 +188,11 @@ def packed_attention(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_
         stream = torch.cuda.current_stream(query.device).cuda_stream
         _lib.check(lib.karpo_attn_fwd(ctypes.byref(args), ctypes.c_void_p(stream)), "packed attention")
     return out
+
+
+# the registered operator (torch.compile, fake tensors, KEPT_OPS); ``run`` calls the implementation directly in eager
+# mode, which saves the dispatcher's ~10 us per call on launch-bound packs
+packed_attention = torch.library.custom_op(f"{NAMESPACE}::packed_attention", mutates_args=())(_packed_attention)
 
 
 @packed_attention.register_fake
@@ -289,9 +293,13 @@ def run(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_cu: Tensor, m
     cos = sin = None
     if rope is not None:
         cos, sin = (_bf16_table(t, query.device) for t in rope)
-    return packed_attention(query, key, value, q_cu, k_cu, int(max_q), float(scale), int(window_left),
-                            int(window_right), spans, tensor, split_tiles, key_rows_of(key_rows), mode, eps, weight,
-                            cos, sin, gate)
+    # the registered operator while dynamo traces or autograd records (it has no gradient: an input that requires
+    # one is torch's error, not a silently detached output); the implementation itself otherwise
+    traced = torch.compiler.is_compiling() or (torch.is_grad_enabled() and (
+        query.requires_grad or key.requires_grad or value.requires_grad))
+    op = packed_attention if traced else _packed_attention
+    return op(query, key, value, q_cu, k_cu, int(max_q), float(scale), int(window_left), int(window_right), spans,
+              tensor, split_tiles, key_rows_of(key_rows), mode, eps, weight, cos, sin, gate)
 
 
 def norm_rope(x: Tensor, norm: Norm | None, rope: tuple[Tensor, Tensor] | None = None,

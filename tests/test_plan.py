@@ -343,3 +343,20 @@ def test_tiny_workload_flops():
     w = workloads.tiny("cpu")
     assert w.pairs() == 184_925
     assert w.flops() == 378_726_400
+
+
+def test_registered_operators_have_fake_kernels():
+    """The operators torch.compile and selective recompute (KEPT_OPS) see: their fake kernels give the real outputs'
+    shapes and dtypes without running anything (eager calls through ops.run skip the dispatcher)."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    with FakeTensorMode():
+        q = torch.empty(10, 4, 64, dtype=torch.bfloat16, device="cuda")
+        k = torch.empty(12, 2, 64, dtype=torch.bfloat16, device="cuda")
+        cu = torch.empty(3, dtype=torch.int32, device="cuda")
+        o = torch.ops.karpo_amd.packed_attention(q, k, k, cu, cu, 8, 0.1, -1, 0, None, None)
+        assert (o.shape, o.dtype) == (q.shape, torch.bfloat16)
+        o, lse = torch.ops.karpo_amd.packed_attention_lse(q, k, k, cu, cu, 8, 0.1, -1, 0, None)
+        assert (lse.shape, lse.dtype) == ((4, 10), torch.float32)
+        dq, dk, dv = torch.ops.karpo_amd.packed_attention_backward(o, q, k, k, o, lse, cu, cu, 8, 0.1, -1, 0, None)
+        assert (dq.shape, dk.shape, dv.shape) == (q.shape, k.shape, k.shape)
