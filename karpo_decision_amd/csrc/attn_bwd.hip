@@ -6,10 +6,10 @@
 //   dV = P^T dO,  dP = dO V^T,  dS = P * (dP - D),  dQ = scale * dS K,  dK = scale * dS^T Q.
 // P and dS enter the MFMAs as bf16 (as P does in the forward), every product accumulates in fp32.
 //
-// Three kernels after the planner (plan_kernel of attn_fwd.hip: both work lists in one launch, no split tiles):
-//   * bwd_stats_kernel: per (head, query row) the log2-domain LSE (+inf for a row that sees no key, so its P are 0)
-//     and D;
-//   * bwd_dq_kernel (query-stationary, the forward's tiles): Q and dO of 32 query vectors per wave as MFMA B operands
+// Two kernels after the planner (plan_kernel of attn_fwd.hip: both work lists in one launch, no split tiles):
+//   * bwd_dq_kernel (query-stationary, the forward's tiles): per (head, query row) first the log2-domain LSE (+inf
+//     for a row that sees no key, so its P are 0) and D = rowsum(dO * O), written for the dK / dV kernel (every
+//     vector is in exactly one query tile); then Q and dO of 32 query vectors per wave as MFMA B operands
 //     in registers, K and V streamed through LDS; S^T = K Q^T and dP^T = V dO^T with K and V read as row operands,
 //     dQ^T += K^T dS^T with K read transposed from the same tile (the S layout of mfma_common.h serves both reads);
 //   * bwd_dkdv_kernel (key-stationary, tiles of 128 keys, four waves of 32): K and V of the wave's keys in registers,
@@ -155,25 +155,37 @@ __global__ __launch_bounds__(64 * bwd_q_waves(D), BwdCfg<D>::BLOCKS_Q) void bwd_
     red[0][wave] = wlo;
     red[1][wave] = whi;
   }
-  // Q and dO as B operands (lane: its vector, elements dc*16 + half*8 .. +8), the row's log2 LSE and D
+  // Q and dO as B operands (lane: its vector, elements dc*16 + half*8 .. +8); the row's log2 LSE and
+  // D = rowsum(dO * O) (the two half-waves hold the two halves of the row), also written for the dK / dV kernel,
+  // which runs after this one (every (row, head) vector is in exactly one query tile)
   bf16x8 qop[DC], dop[DC];
   float lse2 = INFINITY, dsum = 0.f;
   {
     const uint16_t* qp = p.q + (int64_t)(qa + pos) * p.sq_t + (int64_t)head * p.sq_h + half * 8;
-    const uint16_t* op = p.dout + (int64_t)(qa + pos) * p.sdo_t + (int64_t)head * p.sdo_h + half * 8;
+    const uint16_t* dp = p.dout + (int64_t)(qa + pos) * p.sdo_t + (int64_t)head * p.sdo_h + half * 8;
+    const uint16_t* opp = p.o + (int64_t)(qa + pos) * p.so_t + (int64_t)head * p.so_h + half * 8;
+    float part = 0.f;
 #pragma unroll
     for (int dc = 0; dc < DC; ++dc) {
-      u32x4 x = {0, 0, 0, 0}, y = {0, 0, 0, 0};
+      u32x4 x = {0, 0, 0, 0}, y = {0, 0, 0, 0}, z = {0, 0, 0, 0};
       if (valid) {
         x = *(const u32x4*)(qp + dc * 16);
-        y = *(const u32x4*)(op + dc * 16);
+        y = *(const u32x4*)(dp + dc * 16);
+        z = *(const u32x4*)(opp + dc * 16);
       }
       qop[dc] = __builtin_bit_cast(bf16x8, x);
       dop[dc] = __builtin_bit_cast(bf16x8, y);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part = __builtin_fmaf(bf16_at(y, e), bf16_at(z, e), part);
     }
+    dsum = half_swap_sum(part);
     if (valid) {
-      lse2 = p.stats[((int64_t)head * 2) * p.total_q + qa + pos];
-      dsum = p.stats[((int64_t)head * 2 + 1) * p.total_q + qa + pos];
+      const float lse = p.lse[(int64_t)head * p.total_q + qa + pos];
+      lse2 = lse == -INFINITY ? INFINITY : lse * kLog2e;
+      if (half == 0) {
+        p.stats[((int64_t)head * 2) * p.total_q + qa + pos] = lse2;
+        p.stats[((int64_t)head * 2 + 1) * p.total_q + qa + pos] = dsum;
+      }
     }
   }
   __syncthreads();
@@ -609,13 +621,8 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::template occ_k<MODE>()) 
 template <int D>
 static hipError_t launch_bwd_d(const BwdParams& p, const Geometry& gq, const Geometry& gk, int32_t* plan_q,
                                int32_t* plan_k, int64_t items_q, int64_t items_k, hipStream_t stream) {
-  const int64_t vectors = p.total_q * p.heads;
-  const int64_t per_block = 4 * (64 / (D / 8));
-  int64_t blocks = (vectors + per_block - 1) / per_block;
-  if (blocks > 8192) blocks = 8192;
-  if (blocks > 0) hipLaunchKernelGGL(bwd_stats_kernel<D>, dim3((unsigned)blocks), dim3(256), 0, stream, p);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  // the rows' statistics come from the dQ kernel (no separate pass below head size 512)
+  hipError_t e;
   BwdParams pq = p;
   pq.plan = plan_q;
   pq.ng = gq.ng;
