@@ -254,7 +254,8 @@ def main() -> int:
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": f"--gpus {args.gpus}: this build measures one GPU only; the attention kernel "
-                                   "runs on one GPU's share (see DESIGN.md for how it would shard)"}))
+                                   "runs on one GPU's share: (sequence, key/value head) work items are "
+                                   "independent, so a pack shards by heads or by sequences without exchange"}))
         return 2
     import torch
 
