@@ -253,7 +253,7 @@ def backward(args, device, w) -> int:
 def main() -> int:
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": f"--gpus {args.gpus}: this build measures one GPU only; the attention kernel "
+        print(json.dumps({"error": f"--gpus {args.gpus}: the benchmark measures one GPU; the attention kernel "
                                    "runs on one GPU's share: (sequence, key/value head) work items are "
                                    "independent, so a pack shards by heads or by sequences without exchange"}))
         return 2
