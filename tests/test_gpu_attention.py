@@ -324,6 +324,43 @@ def test_windows_and_spans_on_both_sides(gpu):
         assert_close(got, want, f"window ({left}, {right}) with spans")
 
 
+@pytest.mark.parametrize("seed", range(16))
+def test_random_packs_under_every_shape(gpu, seed):
+    """Seeded random packs: sequence lengths (some empty, Lq < Lk for branches), head geometry, head size, window
+    sides, image spans, and a max_q that selects each tile shape the head size has (its runs' longest, or bounds
+    above the small shape's and the wide shape's limits), each call against the oracle."""
+    rng = np.random.default_rng(100 + seed)
+    head = int(rng.choice([64, 128, 256, 512]))
+    kv = int(rng.choice([1, 2, 4]))
+    heads = kv * int(rng.choice([1, 2, 3, 8]))
+    n_seq = int(rng.integers(1, 5))
+    q_lens = [int(x) for x in rng.integers(0, 700, size=n_seq)]
+    k_lens = [ql + (int(rng.integers(0, 300)) if rng.random() < 0.4 else 0) for ql in q_lens]
+    q_cu, k_cu = _lengths_cu(q_lens), _lengths_cu(k_lens)
+    left = int(rng.choice([-1, 0, 17, 200]))
+    right = int(rng.choice([-1, 0, 0, 5]))
+    spans = []
+    if left >= 17 and right == 0 and q_lens[0] > 60:  # an image span inside the first sequence, within the window
+        a = int(rng.integers(0, q_lens[0] - 40))
+        spans = [(a, a + int(rng.integers(2, min(40, left + 2))))]
+    torch.manual_seed(seed)
+    q = (torch.randn(q_cu[-1], heads, head, device=gpu) / 3).bfloat16()
+    k = (torch.randn(k_cu[-1], kv, head, device=gpu) / 3).bfloat16()
+    v = torch.randn(k_cu[-1], kv, head, device=gpu).bfloat16()
+    scale = 1 / math.sqrt(head)
+    want = oa.packed_attention(q.cpu(), k.cpu(), v.cpu(), q_cu, k_cu, scale, left, right, spans)
+    cu_q = torch.tensor(q_cu, dtype=torch.int32, device=gpu)
+    cu_k = torch.tensor(k_cu, dtype=torch.int32, device=gpu)
+    st = torch.tensor(spans, dtype=torch.int32, device=gpu) if spans else None
+    longest = max(q_lens)
+    for max_q in sorted({longest, 9000, 70000}):
+        with torch.inference_mode():
+            got = ops.run(q, k, v, cu_q, cu_k, max_q, scale, left, right, st)
+        shape = _lib.kernel_shape(heads, kv, head, max_q)
+        assert_close(got, want, f"seed {seed}: lengths {q_lens}/{k_lens} H={heads}/{kv} D={head} window "
+                                f"({left}, {right}) spans {spans} max_q {max_q} shape {shape}")
+
+
 def _c_abi_call(q, k, v, o, q_cu, k_cu, max_q, scale, left, right, plan=None):
     lib = _lib.load()
     a = ops._args(q, k, v, o, q_cu, k_cu, q_cu.numel() - 1, max_q, scale, left, right, None, plan)
