@@ -89,6 +89,46 @@ def test_gradients_match_float32(gpu, layout):
         assert r < 2 * rb + 2e-3, (name, r, rb)
 
 
+@pytest.mark.parametrize("seed", range(10))
+def test_random_packs_train(gpu, seed):
+    """Seeded random packs through the differentiable operator: lengths (empty sequences, Lk > Lq branches), head
+    geometry, head sizes 64-512, window sides, an image span; out, dq, dk, dv against autograd through the oracle,
+    to the layouts' criterion."""
+    rng = np.random.default_rng(700 + seed)
+    d = int(rng.choice([64, 128, 256, 512]))
+    kv = int(rng.choice([1, 2, 4]))
+    heads = kv * int(rng.choice([1, 2, 3]))
+    n = int(rng.integers(1, 4))
+    q_lens = [int(x) for x in rng.integers(0, 260, size=n)]
+    k_lens = [ql + (int(rng.integers(0, 120)) if rng.random() < 0.4 else 0) for ql in q_lens]
+    left = int(rng.choice([-1, 0, 17, 90]))
+    right = int(rng.choice([-1, 0, 0, 3]))
+    spans_local = []
+    if left >= 17 and right == 0 and q_lens[0] > 50:
+        a = int(rng.integers(0, q_lens[0] - 30))
+        spans_local = [(0, a, a + int(rng.integers(2, min(30, left + 2))))]
+    q, k, v, do, q_cu, k_cu, spans = make_pack(q_lens, k_lens, heads, kv, d, seed=seed, spans_local=spans_local)
+    scale = d ** -0.5
+    print("case", seed, q_lens, k_lens, heads, kv, d, left, right, spans, flush=True)
+    if max(q_lens) == 0:
+        pytest.skip("an empty pack has no gradients to compare")
+    got = kernel_grads(q, k, v, do, q_cu, k_cu, scale, left, right, spans)
+    want = oa.packed_grads(q, k, v, do, q_cu, k_cu, scale, left, right, spans, dtype=torch.float32)
+    base = oa.packed_grads(q, k, v, do, q_cu, k_cu, scale, left, right, spans, dtype=torch.bfloat16)
+    for name, x, w, b in zip(("out", "dq", "dk", "dv"), got, want, base):
+        assert torch.isfinite(x).all(), name
+        if float(w.float().abs().max()) < 1e-3:
+            # the gradient vanishes in exact arithmetic (window (0, 0): every row sees one key, O = that V row, so
+            # dS = P (dP - D) = 0 and dq, dk are rounding noise in both): the kernel's must be as small
+            print(name, f"vanishing: max-abs {float(x.float().abs().max()):.1e} (oracle {float(w.float().abs().max()):.1e})")
+            assert float(x.float().abs().max()) < 1e-3, name
+            continue
+        r, rb = rel(x, w), rel(b, w)
+        print(name, f"rel {r:.2e} (oracle bf16 {rb:.2e})", flush=True)
+        assert r < REL_FRO, (name, r)
+        assert r < 2 * rb + 2e-3, (name, r, rb)
+
+
 @pytest.mark.parametrize("heads,kv_heads,d", [(8, 2, 128), (4, 2, 64), (4, 2, 256)])
 def test_lse_matches_the_oracle(gpu, heads, kv_heads, d):
     q, k, v, _, q_cu, k_cu, spans = make_pack([300, 40, 0, 77], [300, 20, 0, 90], heads, kv_heads, d, seed=3,
