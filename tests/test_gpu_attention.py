@@ -415,6 +415,37 @@ def test_every_row_is_written_and_device_plan_matches_host_plan(gpu):
     assert torch.equal(o, o2)
 
 
+@pytest.mark.parametrize("n_seq", [1024, 1025, 6000])
+def test_device_plan_of_many_sequences(gpu, n_seq):
+    """Packs of a thousand sequences and more, empty ones among them (the device planner's workgroup scans 1,024
+    sequences per pass): the device work list is the host planner's, and the output matches the oracle on a sample
+    of the sequences."""
+    rng = np.random.default_rng(n_seq)
+    lengths = rng.integers(0, 24, n_seq)
+    lengths[rng.integers(0, n_seq, 3)] = [3000, 1500, 700]
+    cu = _lengths_cu(lengths.tolist())
+    heads, kv_heads, head = 4, 2, 64
+    g = torch.Generator(device="cpu").manual_seed(n_seq)
+    q, k, v = (torch.randn(cu[-1], h, head, generator=g).to(torch.bfloat16).to(gpu) for h in (heads, kv_heads, kv_heads))
+    q_cu = torch.tensor(cu, dtype=torch.int32, device=gpu)
+    max_q = int(lengths.max())
+    o = torch.full_like(q, float("nan"))
+    ws = _c_abi_call(q, k, v, o, q_cu, q_cu, max_q, 0.125, -1, 0)
+    assert not torch.isnan(o).any()
+    plan = ops.make_plan(cu, cu, heads, kv_heads, head, -1, 0, device=gpu, max_q=max_q)
+    host_header, host_merges, host_items = _plan_parts(plan.tensor)
+    dev_header, dev_merges, dev_items = _plan_parts(ws.view(torch.int32)[: plan.tensor.numel()])
+    assert dev_header == host_header
+    assert dev_merges == host_merges
+    assert sorted(dev_items) == sorted(host_items)
+    for s in sorted(set(rng.integers(0, n_seq, 6).tolist()) | {int(np.argmax(lengths))}):
+        a, b = cu[s], cu[s + 1]
+        if a == b:
+            continue
+        want = oa.packed_attention(q[a:b].cpu(), k[a:b].cpu(), v[a:b].cpu(), [0, b - a], [0, b - a], 0.125, -1, 0)
+        assert_close(o[a:b], want, f"{n_seq} sequences: sequence {s} of length {b - a}")
+
+
 def _lengths_cu(lengths):
     cu = [0]
     for n in lengths:
