@@ -188,8 +188,9 @@ def cpu_backward_baseline(w) -> dict:
 
 
 def backward(args, device, w) -> int:
-    """One step = karpo_attn_bwd over the pack (the statistics pass, the dq kernel, the dk/dv kernel and their two
-    planner launches) from a resident output gradient, output and log-sum-exp. TFLOP/s counts the algorithmic
+    """One step = karpo_attn_bwd over the pack (the planner launch for both work lists, the dq kernel, which also
+    writes the per-row statistics, and the dk/dv kernels; at head size 512 a statistics pass first and the wave-pair
+    kernels) from a resident output gradient, output and log-sum-exp. TFLOP/s counts the algorithmic
     backward: 2.5x the forward's FLOPs (five products per visible pair: S, dP, dV, dQ, dK)."""
     import torch
 
@@ -240,7 +241,7 @@ def backward(args, device, w) -> int:
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
                      "kernel": (f"karpo_attn_bwd (bwd_stats_kernel, bwd_dq_pair_kernel<512>, bwd_dkdv_pair_kernel<512>)"
                                 if w.head_dim == 512 else
-                                f"karpo_attn_bwd (bwd_stats_kernel, bwd_dq_kernel<{w.head_dim}>, "
+                                f"karpo_attn_bwd (bwd_dq_kernel<{w.head_dim}>, "
                                 f"bwd_dkdv_kernel<{w.head_dim}, *>)"),
                      "avg_launch_ms": round(launch_ms, 4)},
     }
