@@ -14,6 +14,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import os
 import types
 
 import numpy as np
@@ -324,7 +325,7 @@ def test_windows_and_spans_on_both_sides(gpu):
         assert_close(got, want, f"window ({left}, {right}) with spans")
 
 
-@pytest.mark.parametrize("seed", range(16))
+@pytest.mark.parametrize("seed", range(int(os.environ.get("KARPO_RANDOM_PACKS", "16"))))
 def test_random_packs_under_every_shape(gpu, seed):
     """Seeded random packs: sequence lengths (some empty, Lq < Lk for branches), head geometry, head size, window
     sides, image spans, and a max_q that selects each tile shape the head size has (its runs' longest, or bounds
