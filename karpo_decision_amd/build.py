@@ -24,7 +24,9 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-munsafe-fp-atomics", f"-I{INCLUDE}", f"-I{CSRC}",
 ]
-SOURCES = ["attn_fwd.hip", "attn_bwd.hip", "attn_bwd_pair.hip", "capi.cpp", "plan.cpp"]
+SOURCES = ["attn_fwd.hip", "attn_fwd_128.hip", "attn_bwd.hip", "attn_bwd_pair.hip", "capi.cpp", "plan.cpp"]
+# per-source flags: the head-size-128 wide / long forward tiles under the iterative-ILP machine scheduler
+SOURCE_FLAGS = {"attn_fwd_128.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"]}
 
 
 def hipcc() -> str:
@@ -41,7 +43,7 @@ def build(verbose: bool = False) -> Path:
     objects = []
     for name in SOURCES:
         obj = out / (name + ".o")
-        cmd = [hipcc(), *HIP_FLAGS, "-c", str(CSRC / name), "-o", str(obj)]
+        cmd = [hipcc(), *HIP_FLAGS, *SOURCE_FLAGS.get(name, []), "-c", str(CSRC / name), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)
         done = subprocess.run(cmd, capture_output=True, text=True)

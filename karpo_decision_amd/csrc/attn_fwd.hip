@@ -40,6 +40,13 @@
 #include "mfma_common.h"
 #include "plan_common.h"
 
+// The file builds in two units: unit 0 (this file) holds every kernel but the head-size-128 wide and long tiles,
+// which attn_fwd_128.hip builds as unit 1 under another machine-scheduler strategy; each instantiation is built in
+// exactly one unit, so no kernel name is registered twice.
+#ifndef KA_FWD_UNIT
+#define KA_FWD_UNIT 0
+#endif
+
 namespace karpo {
 
 // Lazy-rescale threshold in log2 units: P values stay below 2^8.
@@ -740,6 +747,7 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(Params p) {
   }
 }
 
+#if KA_FWD_UNIT == 0
 // ---- device planner: one workgroup turns the device bounds into the longest-first work list.
 
 constexpr int kPlanThreads = 1024;
@@ -989,6 +997,8 @@ hipError_t launch_norm_rope(const NormRopeParams& p, int head_dim, hipStream_t s
   return hipGetLastError();
 }
 
+#endif  // KA_FWD_UNIT == 0
+
 // ---- launch
 
 template <int D, int SHAPE>
@@ -1009,16 +1019,17 @@ static hipError_t launch_attn(const Params& p, int64_t items, int64_t merges, in
   return hipGetLastError();
 }
 
+#if KA_FWD_UNIT == 0
 hipError_t launch_forward(const Params& p, int head_dim, const Geometry& g, int64_t items, int64_t merges,
                           hipStream_t stream) {
   if (items <= 0) return hipSuccess;
   switch (head_dim * 4 + g.shape) {  // the shapes tile_shape selects per head size
     case 64 * 4 + kWide: return launch_attn<64, kWide>(p, items, merges, g.n_hg, stream);
     case 64 * 4 + kNarrow: return launch_attn<64, kNarrow>(p, items, merges, g.n_hg, stream);
-    case 128 * 4 + kWide: return launch_attn<128, kWide>(p, items, merges, g.n_hg, stream);
+    case 128 * 4 + kWide: return launch_forward_128(p, kWide, items, merges, g.n_hg, stream);
     case 128 * 4 + kNarrow: return launch_attn<128, kNarrow>(p, items, merges, g.n_hg, stream);
     case 128 * 4 + kSmall: return launch_attn<128, kSmall>(p, items, merges, g.n_hg, stream);
-    case 128 * 4 + kLong: return launch_attn<128, kLong>(p, items, merges, g.n_hg, stream);
+    case 128 * 4 + kLong: return launch_forward_128(p, kLong, items, merges, g.n_hg, stream);
     case 256 * 4 + kWide: return launch_attn<256, kWide>(p, items, merges, g.n_hg, stream);
     case 256 * 4 + kNarrow: return launch_attn<256, kNarrow>(p, items, merges, g.n_hg, stream);
     case 256 * 4 + kSmall: return launch_attn<256, kSmall>(p, items, merges, g.n_hg, stream);
@@ -1034,5 +1045,13 @@ hipError_t launch_plan(const PlanJob* jobs, int n_jobs, int n_seq, hipStream_t s
   hipLaunchKernelGGL(plan_kernel, dim3((unsigned)n_jobs), dim3(kPlanThreads), 0, stream, pj, n_seq);
   return hipGetLastError();
 }
+#else
+hipError_t launch_forward_128(const Params& p, int shape, int64_t items, int64_t merges, int n_hg,
+                              hipStream_t stream) {
+  if (shape == kWide) return launch_attn<128, kWide>(p, items, merges, n_hg, stream);
+  if (shape == kLong) return launch_attn<128, kLong>(p, items, merges, n_hg, stream);
+  return hipErrorInvalidValue;
+}
+#endif  // KA_FWD_UNIT
 
 }  // namespace karpo

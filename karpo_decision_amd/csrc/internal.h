@@ -91,6 +91,9 @@ hipError_t launch_norm_rope(const NormRopeParams& p, int head_dim, hipStream_t s
 // `merges` x head groups, on `stream`.
 hipError_t launch_forward(const Params& p, int head_dim, const Geometry& g, int64_t items, int64_t merges,
                           hipStream_t stream);
+// The head-size-128 wide and long tiles (attn_fwd_128.hip), which launch_forward hands on.
+hipError_t launch_forward_128(const Params& p, int shape, int64_t items, int64_t merges, int n_hg,
+                              hipStream_t stream);
 
 // One work list for the device planner: from the bounds into `plan` (room for `merges` split tiles and `items`
 // items; at most `tiles` tiles are planned), with `tile_base` (n_seq + 1 ints) as its scratch.
