@@ -271,8 +271,10 @@ def main() -> int:
     q_cu = torch.tensor(w.q_cu, dtype=torch.int32, device=device)
     k_cu = torch.tensor(w.k_cu, dtype=torch.int32, device=device)
     spans = torch.tensor(w.spans, dtype=torch.int32, device=device) if w.spans else None
-    plan = ops.make_plan(w.q_cu, w.k_cu, w.heads, w.kv_heads, w.head_dim, w.window_left, w.window_right, device)
     rows = (torch.tensor(w.key_rows, dtype=torch.int32, device=device) if w.key_rows is not None else None)
+    gather = rows is not None and not args.materialize_gather
+    plan = ops.make_plan(w.q_cu, w.k_cu, w.heads, w.kv_heads, w.head_dim, w.window_left, w.window_right, device,
+                         gather=gather)
 
     fused = {}
     if w.q_norm is not None:
@@ -320,7 +322,7 @@ def main() -> int:
         entry = json.loads(TRAFFIC.read_text()).get(w.name)
         if entry:
             traffic = entry.get("bytes_per_launch")
-    shape = _lib.kernel_shape(w.heads, w.kv_heads, w.head_dim, w.max_q)
+    shape = _lib.kernel_shape(w.heads, w.kv_heads, w.head_dim, w.max_q, gather)
     if w.bound(PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)) == "mfma":
         roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_BF16_TFLOPS, 4)}
@@ -338,8 +340,7 @@ def main() -> int:
                    "tokens_per_s": round(w.tokens / (ms_per_step * 1e-3)), "flops_per_step": flops,
                    "min_hbm_bytes_per_step": w.bytes(), "parallelism": "single GPU"},
         "roofline": {**roof, "traffic": traffic,
-                     "kernel": f"attn_fwd_kernel<{w.head_dim}, {shape}, "
-                               f"{str(rows is not None and not args.materialize_gather).lower()}>",
+                     "kernel": f"attn_fwd_kernel<{w.head_dim}, {shape}, {str(gather).lower()}>",
                      "avg_launch_ms": round(launch_ms, 4)},
     }
     if not args.no_cpu_baseline:

@@ -45,8 +45,13 @@ enum {
   KARPO_ATTN_ERR_ARG = 9,         /* a negative size or sequence count */
   KARPO_ATTN_ERR_CAPACITY = 10,   /* karpo_attn_plan: the output buffer is too small */
   KARPO_ATTN_ERR_BOUNDS = 11,     /* karpo_attn_plan: host bounds not non-decreasing from 0 */
-  KARPO_ATTN_ERR_PROLOGUE = 12    /* a norm mode, weight, rope table or gate the kernel cannot take */
+  KARPO_ATTN_ERR_PROLOGUE = 12,   /* a norm mode, weight, rope table or gate the kernel cannot take */
+  KARPO_ATTN_ERR_PLAN = 13        /* a host plan made for another call: its tile geometry, row-table use, sequence
+                                     count or sizes do not match this call's, or its header copy is missing */
 };
+
+/* Int32 entries of a plan's header (see karpo_attn_plan). */
+#define KARPO_ATTN_PLAN_HEADER 12
 
 /* Everything one forward call needs. Tensors are bf16 with head_dim contiguous:
  *   q[total_q, heads, head_dim], k/v[total_k, kv_heads, head_dim], o[total_q, heads, head_dim]
@@ -74,11 +79,13 @@ typedef struct KarpoAttnArgs {
   const int32_t* spans;  /* device, [n_spans][2] half-open query-row ranges [s, e) in pack rows, or NULL */
   int32_t n_spans;       /* spans sorted by start, non-overlapping, each inside one sequence */
   const int32_t* plan;   /* device plan from karpo_attn_plan (copied to the device), or NULL: plan on the device */
+  const int32_t* plan_header; /* host memory: the plan's first KARPO_ATTN_PLAN_HEADER entries as karpo_attn_plan
+                                 wrote them; required with plan. The call is refused (KARPO_ATTN_ERR_PLAN) unless
+                                 they match the call's tile geometry, row-table use, sequence count and sizes; a
+                                 plan that splits no tile (header[4] == 0) needs no workspace. */
   void* workspace;       /* device scratch of karpo_attn_workspace_bytes bytes: the device plan and the partial
                             results of split tiles */
   size_t workspace_bytes;
-  int32_t plan_unsplit;  /* nonzero when args->plan splits no tile (its plan[4] == 0): the merge kernel is not
-                            launched. 0 (always safe) when unknown. Ignored without a plan. */
   const int32_t* k_rows; /* device, k_cu[n_seq] row indices, or NULL: key j of sequence i is row k_rows[k_cu[i] + j]
                             of k and v (the gathered branch keys of a block plan, read in place) instead of row
                             k_cu[i] + j. Rows outside [0, total_k) read as zeros. */
@@ -109,6 +116,12 @@ typedef struct KarpoAttnArgs {
    * lse[h * total_q + row] = ln(sum over the row's visible keys of exp(scale * q.k)), -inf for a row that sees none.
    * Not with a gate (the gate's own gradient is not this library's). */
   float* lse;                   /* device fp32 [heads][total_q], or NULL */
+
+  /* The query the attention used, written when the fused prologue runs (its normalised, rotated bf16 vectors: the
+   * reference's q after fused.norm_rope, which its backward differentiates through; a training forward keeps it).
+   * Only with q_norm or rope_cos set. */
+  void* q_out;                  /* device bf16 [total_q][heads][head_dim] with the strides below, or NULL */
+  int64_t q_out_stride_tok, q_out_stride_head;
 } KarpoAttnArgs;
 
 /* Query / key normalisations of the fused prologue and of karpo_attn_norm_rope. */
@@ -164,10 +177,10 @@ typedef struct KarpoAttnBwdArgs {
 int karpo_attn_bwd_workspace_bytes(const KarpoAttnBwdArgs* args, size_t* bytes);
 int karpo_attn_bwd(const KarpoAttnBwdArgs* args, void* stream);
 
-/* Bytes of device workspace karpo_attn_fwd needs for these arguments (reads only sizes: heads, kv_heads, head_dim,
- * n_seq, total_q, max_q). It holds the device plan (when args->plan is NULL) and the fp32 partial results of tiles
- * the plan splits over their keys; only a call with a host plan marked plan_unsplit may pass none. Calls that
- * overlap on one device need separate workspaces. */
+/* Bytes of device workspace karpo_attn_fwd needs for these arguments (reads only sizes and whether k_rows is set:
+ * heads, kv_heads, head_dim, n_seq, total_q, max_q). It holds the device plan (when args->plan is NULL), the device
+ * planner's status word and the fp32 partial results of tiles the plan splits over their keys; only a call with a
+ * host plan that splits no tile may pass none. Calls that overlap on one device need separate workspaces. */
 int karpo_attn_workspace_bytes(const KarpoAttnArgs* args, size_t* bytes);
 
 /* Int32 entries a plan buffer for these arguments holds at most (the capacity to give karpo_attn_plan). */
@@ -175,30 +188,44 @@ int karpo_attn_plan_capacity(const KarpoAttnArgs* args, int64_t* entries);
 
 /* The forward pass on `stream` (a hipStream_t; NULL is the null stream): the device planner unless args->plan is set,
  * the attention kernel, and the merge kernel that combines the parts of split tiles. Replaces
- * triton_attention.attend's launch (triton_attention.py:103-109); the caller owns o. */
+ * triton_attention.attend's launch (triton_attention.py:103-109); the caller owns o. Every row of every head inside
+ * the sequences' bounds is written: a host plan is checked against the call before anything is launched, and the
+ * device planner's capacities hold for any bounds that keep the contract (non-decreasing from 0, query rows within
+ * total_q, every query run at most max_q); device bounds that break it are not planned (nothing is launched past the
+ * planner, no row is read or written) and leave KARPO_ATTN_ERR_BOUNDS in the workspace's status word. */
 int karpo_attn_fwd(const KarpoAttnArgs* args, void* stream);
+
+/* The status word the device planner of the last karpo_attn_fwd call on this workspace (args->plan NULL) left:
+ * KARPO_ATTN_OK, or KARPO_ATTN_ERR_BOUNDS when the device bounds broke the contract and nothing was computed.
+ * Copies one word to the host and synchronises `stream`: for tests and debugging (the forward never waits for the
+ * device, so it cannot return this status itself). */
+int karpo_attn_device_status(const KarpoAttnArgs* args, void* stream, int32_t* status);
 
 /* The work list on the host from host copies of the bounds, in the layout the kernels read:
  *   plan[0] = work items, plan[1] = query rows per tile, plan[2] = keys per step, plan[3] = heads per work item,
  *   plan[4] = split tiles, plan[5] = waves per workgroup, plan[6] = offset of the first item, plan[7] = partial
- *   slots used;
- *   at plan[8]: per split tile (segment, tile, parts, first partial slot), in segment, tile order;
+ *   slots used, plan[8] = sequences, plan[9] = 1 when the calls read keys through a row table (else 0),
+ *   plan[10] = tile shape (0 wide, 1 one-wave, 2 four-wave, 3 long), plan[11] = 0;
+ *   at plan[KARPO_ATTN_PLAN_HEADER]: per split tile (segment, tile, parts, first partial slot), in segment, tile
+ *   order;
  *   at plan[plan[6]]: per item (segment, tile, part | parts << 16, first partial slot or -1), longest first (ties in
  *   segment, tile, part order).
  * A tile visits the key steps its queries can see; one whose steps exceed the pack's per-workgroup share is split
  * into parts over those steps (the policy depends only on the bounds and the tile shape). Replaces the host-side
  * bound building of block_plan (families/gemma/packed.py:103-151); like it, it runs once per pack and its result is
- * reused by every layer of the same geometry. Reads heads, kv_heads, head_dim, max_q, window_*; a plan is only valid
- * for karpo_attn_fwd calls with the same values (max_q selects the tile shape). */
+ * reused by every layer of the same geometry. Reads heads, kv_heads, head_dim, max_q, window_* and whether k_rows is
+ * set (calls through a row table take the four-wave tiles at head sizes 128 and 256); a plan is only valid for
+ * karpo_attn_fwd calls with the same values (max_q selects the tile shape) and the same sequence count. */
 int karpo_attn_plan(const KarpoAttnArgs* args, const int32_t* q_cu_host, const int32_t* k_cu_host, int32_t n_seq,
                     int32_t* plan, int64_t capacity);
 
-/* Query rows per tile, keys per step and query heads per work item the kernel uses for these heads / head size and
- * the longest query run max_q: packs whose sequences fit one wave's 32 query vectors take one-wave tiles; runs up to
- * 4,096 queries at head size 128 (8,192 at 256) take 4-wave tiles; longer ones the wide tiles (12 waves at 128, 32
- * keys per step; 64 keys per step above 65,536 queries). */
-int karpo_attn_tile_shape(int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t max_q, int32_t* rows_per_tile,
-                          int32_t* keys_per_step, int32_t* heads_per_item);
+/* Query rows per tile, keys per step and query heads per work item the kernel uses for these heads / head size, the
+ * longest query run max_q and row-table use (gather nonzero: the call sets k_rows): packs whose sequences fit one
+ * wave's 32 query vectors take one-wave tiles; runs up to 4,096 queries at head size 128 (8,192 at 256), and every
+ * run read through a row table at those head sizes, take 4-wave tiles; longer ones the wide tiles (12 waves at 128,
+ * 32 keys per step; 64 keys per step above 65,536 queries). */
+int karpo_attn_tile_shape(int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t max_q, int32_t gather,
+                          int32_t* rows_per_tile, int32_t* keys_per_step, int32_t* heads_per_item);
 
 /* A static message for a status code. */
 const char* karpo_attn_strerror(int status);

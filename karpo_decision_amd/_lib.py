@@ -1,4 +1,4 @@
-"""ctypes binding of ``libkarpo_attn.so`` (``include/karpo_attn.h``, version 2). The library is the only compute path: if it is
+"""ctypes binding of ``libkarpo_attn.so`` (``include/karpo_attn.h``, version 3). The library is the only compute path: if it is
 missing this module raises, it never falls back to another implementation."""
 
 from __future__ import annotations
@@ -12,14 +12,16 @@ LIBRARY = Path(__file__).resolve().parent / "libkarpo_attn.so"
 #: Every symbol ``include/karpo_attn.h`` declares.
 EXPORTS = ("karpo_attn_fwd", "karpo_attn_plan", "karpo_attn_plan_capacity", "karpo_attn_workspace_bytes",
            "karpo_attn_tile_shape", "karpo_attn_strerror", "karpo_attn_version", "karpo_attn_norm_rope",
-           "karpo_attn_bwd_workspace_bytes", "karpo_attn_bwd")
+           "karpo_attn_bwd_workspace_bytes", "karpo_attn_bwd", "karpo_attn_device_status")
 
 OK = 0
 ERR_HEAD_DIM, ERR_HEADS, ERR_LAYOUT, ERR_WINDOW, ERR_SPANS, ERR_ARG, ERR_BOUNDS = 2, 3, 4, 6, 7, 9, 11
-ERR_PROLOGUE = 12
+ERR_PROLOGUE, ERR_PLAN = 12, 13
+#: Int32 entries of a plan's header (KARPO_ATTN_PLAN_HEADER).
+PLAN_HEADER = 12
 #: Status codes that mean "these arguments are not supported" (ValueError), the rest are runtime failures.
 VALUE_ERRORS = {1, ERR_HEAD_DIM, ERR_HEADS, ERR_LAYOUT, 5, ERR_WINDOW, ERR_SPANS, ERR_ARG, 10, ERR_BOUNDS,
-                ERR_PROLOGUE}
+                ERR_PROLOGUE, ERR_PLAN}
 
 
 class KarpoAttnArgs(ctypes.Structure):
@@ -35,12 +37,14 @@ class KarpoAttnArgs(ctypes.Structure):
         ("total_q", ctypes.c_int64), ("max_q", ctypes.c_int32), ("scale", ctypes.c_float),
         ("window_left", ctypes.c_int32), ("window_right", ctypes.c_int32),
         ("spans", ctypes.c_void_p), ("n_spans", ctypes.c_int32),
-        ("plan", ctypes.c_void_p), ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
-        ("plan_unsplit", ctypes.c_int32), ("k_rows", ctypes.c_void_p), ("total_k", ctypes.c_int64),
+        ("plan", ctypes.c_void_p), ("plan_header", ctypes.POINTER(ctypes.c_int32)),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+        ("k_rows", ctypes.c_void_p), ("total_k", ctypes.c_int64),
         ("q_norm", ctypes.c_int32), ("q_norm_eps", ctypes.c_float), ("q_norm_weight", ctypes.c_void_p),
         ("rope_cos", ctypes.c_void_p), ("rope_sin", ctypes.c_void_p), ("rope_stride", ctypes.c_int64),
         ("rope_dim", ctypes.c_int32), ("gate", ctypes.c_void_p), ("gate_stride_tok", ctypes.c_int64),
         ("gate_stride_head", ctypes.c_int64), ("lse", ctypes.c_void_p),
+        ("q_out", ctypes.c_void_p), ("q_out_stride_tok", ctypes.c_int64), ("q_out_stride_head", ctypes.c_int64),
     ]
 
 
@@ -92,7 +96,8 @@ def load() -> ctypes.CDLL:
         lib.karpo_attn_workspace_bytes.argtypes = [P(KarpoAttnArgs), P(ctypes.c_size_t)]
         lib.karpo_attn_workspace_bytes.restype = ctypes.c_int
         lib.karpo_attn_tile_shape.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
-                                              P(ctypes.c_int32), P(ctypes.c_int32), P(ctypes.c_int32)]
+                                              ctypes.c_int32, P(ctypes.c_int32), P(ctypes.c_int32),
+                                              P(ctypes.c_int32)]
         lib.karpo_attn_tile_shape.restype = ctypes.c_int
         lib.karpo_attn_strerror.argtypes = [ctypes.c_int]
         lib.karpo_attn_strerror.restype = ctypes.c_char_p
@@ -104,6 +109,8 @@ def load() -> ctypes.CDLL:
         lib.karpo_attn_bwd_workspace_bytes.restype = ctypes.c_int
         lib.karpo_attn_bwd.argtypes = [P(KarpoAttnBwdArgs), ctypes.c_void_p]
         lib.karpo_attn_bwd.restype = ctypes.c_int
+        lib.karpo_attn_device_status.argtypes = [P(KarpoAttnArgs), ctypes.c_void_p, P(ctypes.c_int32)]
+        lib.karpo_attn_device_status.restype = ctypes.c_int
         _lib = lib
         return lib
 
@@ -124,11 +131,11 @@ def check(status: int, what: str) -> None:
 LONG = 1 << 30
 
 
-def kernel_shape(heads: int, kv_heads: int, head_dim: int, max_q: int = LONG) -> int:
-    """The forward kernel's tile-shape template argument for these heads and longest query run (0 wide, 1 narrow: one
-    wave, or one pair at head_dim 512; 2 small: four waves at head_dim 128 / 256; 3 long: 64-key steps at 128), as
-    read off tile_shape's geometry."""
-    rows, keys, per = tile_shape(heads, kv_heads, head_dim, max_q)
+def kernel_shape(heads: int, kv_heads: int, head_dim: int, max_q: int = LONG, gather: bool = False) -> int:
+    """The forward kernel's tile-shape template argument for these heads, longest query run and row-table use (0
+    wide, 1 narrow: one wave, or one pair at head_dim 512; 2 small: four waves at head_dim 128 / 256; 3 long: 64-key
+    steps at 128), as read off tile_shape's geometry."""
+    rows, keys, per = tile_shape(heads, kv_heads, head_dim, max_q, gather)
     vectors = rows * per
     waves = vectors // 32 * (2 if head_dim == 512 else 1)
     if vectors == 32:
@@ -140,10 +147,11 @@ def kernel_shape(heads: int, kv_heads: int, head_dim: int, max_q: int = LONG) ->
     return 0
 
 
-def tile_shape(heads: int, kv_heads: int, head_dim: int, max_q: int = LONG) -> tuple[int, int, int]:
+def tile_shape(heads: int, kv_heads: int, head_dim: int, max_q: int = LONG,
+               gather: bool = False) -> tuple[int, int, int]:
     """(query rows per tile, keys per step, query heads per work item) for packs whose longest query run is
-    ``max_q`` (one-wave tiles when every run fits one)."""
+    ``max_q`` (one-wave tiles when every run fits one), read through a row table when ``gather``."""
     rows, keys, per = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
-    check(load().karpo_attn_tile_shape(heads, kv_heads, head_dim, max_q, ctypes.byref(rows), ctypes.byref(keys),
-                                       ctypes.byref(per)), "karpo_attn_tile_shape")
+    check(load().karpo_attn_tile_shape(heads, kv_heads, head_dim, max_q, int(bool(gather)), ctypes.byref(rows),
+                                       ctypes.byref(keys), ctypes.byref(per)), "karpo_attn_tile_shape")
     return rows.value, keys.value, per.value

@@ -8,6 +8,7 @@ from __future__ import annotations
 import os
 import shutil
 import subprocess
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PACKAGE = Path(__file__).resolve().parent
@@ -36,24 +37,29 @@ def hipcc() -> str:
     return found
 
 
+def _compile(name: str, out: Path, verbose: bool) -> str:
+    obj = out / (name + ".o")
+    cmd = [hipcc(), *HIP_FLAGS, *SOURCE_FLAGS.get(name, []), "-c", str(CSRC / name), "-o", str(obj)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    done = subprocess.run(cmd, capture_output=True, text=True)
+    errors = "\n".join(line for line in (done.stdout + done.stderr).splitlines()
+                       if "packed-fp32-ops" not in line)  # hipcc's host pass does not know the feature
+    if done.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {name}:\n{errors}")
+    if verbose and errors.strip():
+        print(errors)
+    return str(obj)
+
+
 def build(verbose: bool = False) -> Path:
-    """Compiles every source and links the shared library; returns its path. Always rebuilds."""
+    """Compiles every source (one hipcc process per source, side by side) and links the shared library; returns its
+    path. Always rebuilds."""
     out = PACKAGE / "_build"
     out.mkdir(exist_ok=True)
-    objects = []
-    for name in SOURCES:
-        obj = out / (name + ".o")
-        cmd = [hipcc(), *HIP_FLAGS, *SOURCE_FLAGS.get(name, []), "-c", str(CSRC / name), "-o", str(obj)]
-        if verbose:
-            print(" ".join(cmd), flush=True)
-        done = subprocess.run(cmd, capture_output=True, text=True)
-        errors = "\n".join(line for line in (done.stdout + done.stderr).splitlines()
-                           if "packed-fp32-ops" not in line)  # hipcc's host pass does not know the feature
-        if done.returncode != 0:
-            raise RuntimeError(f"hipcc failed on {name}:\n{errors}")
-        if verbose and errors.strip():
-            print(errors)
-        objects.append(str(obj))
+    workers = max(1, min(len(SOURCES), int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        objects = list(pool.map(lambda name: _compile(name, out, verbose), SOURCES))
     tmp = LIBRARY.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objects, "-o", str(tmp)]
     done = subprocess.run(cmd, capture_output=True, text=True)

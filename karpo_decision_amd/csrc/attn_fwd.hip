@@ -23,8 +23,9 @@
 //   * LDS tiles are blocked so that every 16 lanes of an LDS read touch one contiguous 256-byte run (conflict-free on
 //     the 64 banks): K as [16-key block][16-byte chunk][16 keys], V as [4-key group][16-wide d block][4 keys][16 d];
 //     every per-step address is a lane base plus an immediate offset;
-//   * the running maximum is only raised when a step's maximum exceeds it by more than 2^8 (exact: the final
-//     division by l cancels any common factor), so O is rescaled on few steps;
+//   * the running maximum is only raised when a step's maximum exceeds it by more than a factor 2^8 (exact: the final
+//     division by l cancels any common factor), so O is rescaled on few steps; at logit scales of order one (a
+//     peaked softmax) it is kept exact instead (p.tau, chosen by the host);
 //   * a part of a split tile stores its unnormalised fp32 O, running maximum m and sum l; merge_kernel combines the
 //     parts as O = sum_p 2^(m_p - M) O_p / sum_p 2^(m_p - M) l_p with M = max_p m_p;
 //   * at head_dim 512 one wave cannot hold 32 vectors' O (256 fp32 per lane) beside their Q operands, so a pair of
@@ -49,8 +50,6 @@
 
 namespace karpo {
 
-// Lazy-rescale threshold in log2 units: P values stay below 2^8.
-constexpr float kTau = 8.0f;
 // Per head size and tile shape (TileShape of plan_common.h): waves (W), keys per step (BN) and waves per SIMD the
 // registers are budgeted for (OCC). Wide: D=64 4-wave workgroups, four per CU; D=128 one 12-wave workgroup per CU
 // (three waves per SIMD) sharing one 32-key K/V stream (64-key steps in the long shape), 32 KiB LDS (64 KiB); D=256
@@ -151,6 +150,7 @@ __device__ __forceinline__ void query_prologue(const Params& p, const uint16_t* 
         n[e] = norm ? round_bf16(h * r * __builtin_fmaf(wm, bf16_at(wv[j], e), wa)) : h;
       }
       if (rot) {
+#pragma clang fp contract(off)  // x cos + rot(x) sin: both products rounded, then the sum, as the reference
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const float hp = bf16_at(pr[j], e);
@@ -195,6 +195,7 @@ __device__ __forceinline__ void query_prologue_regs(const Params& p, int64_t qro
         float a[2], b[2];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
+#pragma clang fp contract(off)  // x cos + rot(x) sin: both products rounded, then the sum, as the reference
           const int e = 2 * t + u;
           const float n0 = bf16_at(x[i], e), n1 = bf16_at(x[i + RC / 2], e);
           a[u] = n0 * bf16_at(c0, e) - n1 * bf16_at(s0, e);
@@ -246,7 +247,7 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
   // five workgroups' 80; the markers layer's attention kernel 115.9 -> 109.6 us, planned two per CU either way); the
   // others two buffers. The deeper ring counts its own copies to wait for one step's, so it is only built where every
   // copy instruction is issued unconditionally (one wave, no row table).
-  constexpr int NB = SHAPE == kNarrow && W == 1 && !GATHER && D <= 128 ? 4 : 2;
+  constexpr int NB = kv_buffers(D, SHAPE, GATHER);
   static_assert(NB == 2 || (W == 1 && BLKS == INSTS), "the ring waits on a fixed count of its wave's copies");
   constexpr int CPS = 2 * INSTS;  // copy instructions per step of a one-wave tile (K and V)
   static_assert(NB == 2 || (NB - 2) * CPS <= 63, "vmcnt counts at most 63 outstanding operations");
@@ -288,7 +289,6 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
   const int rows_per_tile = p.plan[1];
   const int qa = p.q_cu[seg], lq = p.q_cu[seg + 1] - qa;
   const int ka = p.k_cu[seg], lk = p.k_cu[seg + 1] - ka;
-  const int delta = lk - lq;
   const int kvh = (hg * p.ng) / p.group;
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -305,35 +305,20 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
   int lo = 0, hi = 0, sl = 0, sh = 0;
   int wlo = INT32_MAX, whi = INT32_MIN, wflo = INT32_MIN, wfhi = INT32_MAX;
   if (valid) {
-    const int ip = pos + delta;  // aligned key coordinate
-    int a = p.left < 0 ? 0 : max(0, ip - p.left);
-    int b = p.right < 0 ? lk : (int)min((int64_t)lk, (int64_t)ip + p.right + 1);
-    if (b < a) b = a;
-    lo = a;
-    hi = b;
-    wflo = a;
-    wfhi = b;
-    if (a < b) {
-      wlo = a;
-      whi = b;
+    const LaneKeys lk_ = lane_keys(pos, qa, lq, lk, p.left, p.right, p.spans, p.n_spans);
+    lo = lk_.lo;
+    hi = lk_.hi;
+    sl = lk_.sl;
+    sh = lk_.sh;
+    wflo = lo;
+    wfhi = hi;
+    if (lo < hi) {
+      wlo = lo;
+      whi = hi;
     }
-    if (p.n_spans > 0) {  // the last span starting at or before this query row
-      const int row = qa + pos;
-      int l0 = 0, l1 = p.n_spans;
-      while (l1 - l0 > 1) {
-        const int mid = (l0 + l1) >> 1;
-        if (p.spans[2 * mid] <= row) l0 = mid; else l1 = mid;
-      }
-      const int s0 = p.spans[2 * l0], s1 = p.spans[2 * l0 + 1];
-      if (s0 <= row && row < s1) {
-        const int x = max(0, s0 - qa + delta), y = min(lk, s1 - qa + delta);
-        if (x < y) {
-          sl = x;
-          sh = y;
-          wlo = min(wlo, x);
-          whi = max(whi, y);
-        }
-      }
+    if (sl < sh) {
+      wlo = min(wlo, sl);
+      whi = max(whi, sh);
     }
   }
   wlo = __builtin_amdgcn_readfirstlane(wave_min(wlo));
@@ -360,6 +345,11 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
     }
     if (p.q_norm != KARPO_NORM_NONE || p.rope_cos != nullptr) {
       if (valid) query_prologue<D, QC>(p, qrow, (int64_t)(qa + pos), half, dh * QC, x);
+      if (p.q_out != nullptr && valid && part == 0) {  // the attention's query, once per (row, head)
+        uint16_t* qo = p.q_out + (int64_t)(qa + pos) * p.sqo_t + (int64_t)head * p.sqo_h + half * 8;
+#pragma unroll
+        for (int i = 0; i < QC; ++i) *(u32x4*)(qo + (dh * QC + i) * 16) = x[i];
+      }
     }
 #pragma unroll
     for (int i = 0; i < QC; ++i) qop[i] = __builtin_bit_cast(bf16x8, x[i] ^ p.qsign);
@@ -376,13 +366,8 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
     klo = __builtin_amdgcn_readfirstlane(klo);
     khi = __builtin_amdgcn_readfirstlane(khi);
   }
-  int j_first = klo < khi ? (klo / BN) * BN : 0;
-  int n_steps = klo < khi ? (khi - j_first + BN - 1) / BN : 0;
-  if (parts > 1) {  // this part's share of the envelope's steps (possibly none)
-    const int s0 = (int)((int64_t)part * n_steps / parts), s1 = (int)((int64_t)(part + 1) * n_steps / parts);
-    j_first += s0 * BN;
-    n_steps = s1 - s0;
-  }
+  int j_first, n_steps;  // the envelope's steps, or this part's share of them (possibly none)
+  part_steps(klo, khi, BN, part, parts, &j_first, &n_steps);
 
   // ---- DMA: per instruction a lane's byte offset inside the step's rows (fixed for the kernel). Each step's rows
   // are one buffer resource starting at the step's first key row, sized to the rows that exist: reads past the
@@ -422,8 +407,8 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
       }
     }
   };
-  auto gathered = [&](int row, uint32_t colb, int64_t stride) -> uint32_t {
-    return (unsigned)row < (unsigned)p.total_k ? (uint32_t)row * (uint32_t)(stride * 2) + colb : 0xffffffffu;
+  auto gathered = [&](int row, uint32_t colb, int64_t stride, uint32_t bytes) -> uint32_t {
+    return gather_offset(row, p.total_k, (uint32_t)(stride * 2), colb, bytes);
   };
   // copies run in step order: the step's first key row pointers advance by increments (no per-step multiply)
   const uint16_t* c_k = kbase + (GATHER ? 0 : (int64_t)j_first * p.sk_t);
@@ -437,7 +422,7 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
     for (int r = 0; r < INSTS; ++r)
       if (BLKS % W == 0 || wave * INSTS + r < BLKS) {
         if constexpr (GATHER)
-          dma_16b(ks, (int)p.k_bytes, kt + (wave * INSTS + r) * 1024, gathered(k_row[r], k_voff[r], p.sk_t));
+          dma_16b(ks, (int)p.k_bytes, kt + (wave * INSTS + r) * 1024, gathered(k_row[r], k_voff[r], p.sk_t, p.k_bytes));
         else
           dma_16b(ks, rows * (int)p.sk_t * 2, kt + (wave * INSTS + r) * 1024, k_voff[r]);
       }
@@ -450,7 +435,7 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
     for (int r = 0; r < INSTS; ++r)
       if (BLKS % W == 0 || wave * INSTS + r < BLKS) {
         if constexpr (GATHER)
-          dma_16b(vs, (int)p.v_bytes, vt + (wave * INSTS + r) * 1024, gathered(v_row[r], v_voff[r], p.sv_t));
+          dma_16b(vs, (int)p.v_bytes, vt + (wave * INSTS + r) * 1024, gathered(v_row[r], v_voff[r], p.sv_t, p.v_bytes));
         else
           dma_16b(vs, rows * (int)p.sv_t * 2, vt + (wave * INSTS + r) * 1024, v_voff[r]);
       }
@@ -590,7 +575,7 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
 #pragma unroll
         for (int jj = 0; jj < 16; ++jj) mx = fmaxf(mx, st[kb][jj]);
       const float mt = half_swap_max(mx) * c;
-      const bool need = mt > m + kTau;
+      const bool need = mt > m + p.tau;
       if (__builtin_amdgcn_ballot_w64(need)) {  // raise the running maximum (rare after the first steps)
         const float mn = need ? mt : m;
         const float alpha = need ? __builtin_amdgcn_exp2f(m - mn) : 1.f;  // m = -inf, mt finite: alpha = 0
@@ -656,7 +641,7 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
   const float lt = half_swap_sum(l);
   if (parts > 1) {  // one part of a split tile: unnormalised fp32 O, m and l for merge_kernel
     constexpr int V = tile_vectors(D, SHAPE);
-    float* base = p.partial + ((int64_t)(slot + part) * p.n_hg + hg) * (int64_t)V * (D + 2);
+    float* base = p.partial + partial_base(slot, part, p.n_hg, hg, V, D);
     float* op = base + (int64_t)vec * D + dh * (D / 2) + half * 4;
 #pragma unroll
     for (int db = 0; db < OB; ++db)
@@ -811,6 +796,32 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanJobs jobs, int n
   __shared__ int scratch[kPlanThreads / 64 + 1];
   __shared__ int64_t scratch64[kPlanThreads / 64];
   const int tid = threadIdx.x;
+  // the header's constant entries (an empty plan until the items are listed)
+  if (tid == 0) {
+    plan[0] = 0;
+    plan[1] = g.rows;
+    plan[2] = g.bn;
+    plan[3] = g.ng;
+    plan[4] = 0;
+    plan[5] = g.waves;
+    plan[6] = kPlanHeader;
+    plan[7] = 0;
+    plan[8] = n_seq;
+    plan[9] = job.gather;
+    plan[10] = g.shape;
+    plan[11] = 0;
+  }
+  if (job.status != nullptr) {  // the bounds against the call's contract: a violation plans nothing
+    int bad = 0;
+    for (int i = tid; i < n_seq; i += kPlanThreads) {
+      const int q0 = q_cu[i], q1 = q_cu[i + 1], k0 = k_cu[i], k1 = k_cu[i + 1];
+      bad |= q0 < 0 || k0 < 0 || q1 < q0 || k1 < k0 || q1 - q0 > job.max_q || (int64_t)q1 > job.total_q;
+    }
+    int total;
+    block_exclusive_scan(bad, &total, scratch);
+    if (tid == 0) *job.status = total > 0 ? KARPO_ATTN_ERR_BOUNDS : KARPO_ATTN_OK;
+    if (total > 0) return;
+  }
   int carry = 0;
   for (int base = 0; base < n_seq; base += kPlanThreads) {
     const int i = base + tid;
@@ -909,13 +920,10 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanJobs jobs, int n
   }
   if (tid == 0) {
     plan[0] = fits ? n_items : 0;
-    plan[1] = g.rows;
-    plan[2] = g.bn;
-    plan[3] = g.ng;
     plan[4] = fits ? n_merges : 0;
-    plan[5] = g.waves;
-    plan[6] = first;
-    plan[7] = slot_carry;
+    plan[6] = fits ? first : kPlanHeader;
+    plan[7] = fits ? slot_carry : 0;
+    if (!fits && job.status != nullptr) *job.status = KARPO_ATTN_ERR_CAPACITY;  // unreachable within the contract
   }
 }
 
@@ -967,6 +975,7 @@ __global__ __launch_bounds__(64 * kNormRopeWaves) void norm_rope_kernel(NormRope
       }
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
+#pragma clang fp contract(off)  // x cos + rot(x) sin: both products rounded, then the sum, as the reference
         const float pn = __shfl(n[e], src);
         const float y = n[e] * bf16_at(cv, e) + sgn * pn * bf16_at(sv, e);
         n[e] = in ? y : n[e];
@@ -1001,13 +1010,20 @@ hipError_t launch_norm_rope(const NormRopeParams& p, int head_dim, hipStream_t s
 
 // ---- launch
 
+// Whether a shape is built with a row table: every shape but the wide and long tiles at head sizes 128 and 256,
+// which tile_shape never selects for a call with a row table.
+constexpr bool gather_built(int d, int shape) { return !((d == 128 || d == 256) && (shape == kWide || shape == kLong)); }
+
 template <int D, int SHAPE>
 static hipError_t launch_attn(const Params& p, int64_t items, int64_t merges, int n_hg, hipStream_t stream) {
   using Cfg = TileCfg<D, SHAPE>;
-  if (p.k_rows != nullptr)
-    hipLaunchKernelGGL((attn_fwd_kernel<D, SHAPE, true>), dim3((unsigned)(items * n_hg)), dim3(64 * Cfg::W), 0,
-                       stream, p);
-  else
+  if (p.k_rows != nullptr) {
+    if constexpr (gather_built(D, SHAPE))
+      hipLaunchKernelGGL((attn_fwd_kernel<D, SHAPE, true>), dim3((unsigned)(items * n_hg)), dim3(64 * Cfg::W), 0,
+                         stream, p);
+    else
+      return hipErrorInvalidValue;
+  } else
     hipLaunchKernelGGL((attn_fwd_kernel<D, SHAPE, false>), dim3((unsigned)(items * n_hg)), dim3(64 * Cfg::W), 0,
                        stream, p);
   hipError_t e = hipGetLastError();

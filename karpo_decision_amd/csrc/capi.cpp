@@ -26,33 +26,38 @@ int check_shape(const KarpoAttnArgs* a) {
   return KARPO_ATTN_OK;
 }
 
-// Tiles a launch covers at most: every sequence adds at most one partial tile, and none has more than max_q rows.
 int64_t tile_capacity(const KarpoAttnArgs* a, const Geometry& g) {
-  const int64_t by_rows = (a->total_q + g.rows - 1) / g.rows + a->n_seq;
-  const int64_t by_max = (int64_t)a->n_seq * tiles_of(a->max_q, g.rows);
-  return by_rows < by_max ? by_rows : by_max;
+  return karpo::tile_capacity(a->total_q, a->n_seq, a->max_q, g);
 }
 
-// Sizes of one call's plan and workspace. Items: every unsplit tile once plus the parts of split tiles (fewer than
-// split_slots); split tiles: fewer than half the slots.
-struct Sizes {
-  int64_t tiles, items, merges, plan_entries, partial_offset, bytes;
-};
+// The forward's tile geometry for these arguments (a row table takes the four-wave tiles at head sizes 128 / 256).
+Geometry fwd_geometry(const KarpoAttnArgs* a) {
+  return geometry(a->heads, a->kv_heads, a->head_dim, a->max_q, a->k_rows != nullptr);
+}
 
-Sizes sizes_of(const KarpoAttnArgs* a, const Geometry& g) {
-  Sizes z;
-  z.tiles = tile_capacity(a, g);
-  z.items = z.tiles + split_slots(g);
-  z.merges = ka_min(z.tiles, split_tiles(g));
-  z.plan_entries = kPlanHeader + kMergeInts * z.merges + kItemInts * z.items;
-  const int64_t ints = z.plan_entries + (int64_t)a->n_seq + 1;  // plan, then the planner's tile bases
-  z.partial_offset = (ints * 4 + 255) / 256 * 256;
-  const int64_t partial = split_slots(g) * g.n_hg * (int64_t)g.vectors * (a->head_dim + 2) * 4;
-  z.bytes = z.partial_offset + (partial + 255) / 256 * 256;
-  return z;
+FwdSizes sizes_of(const KarpoAttnArgs* a, const Geometry& g) {
+  return fwd_sizes(a->total_q, a->n_seq, a->max_q, a->head_dim, g);
+}
+
+// A host plan's header against the call: the same tile geometry, row-table use and sequence count, and counts
+// within the launch's capacities (the items, split tiles and partial slots the grid, merge launch and workspace
+// cover), with the items right after the split tiles. Anything else would leave rows unwritten.
+bool plan_matches(const int32_t* h, const KarpoAttnArgs* a, const Geometry& g, const FwdSizes& z) {
+  return h[1] == g.rows && h[2] == g.bn && h[3] == g.ng && h[5] == g.waves && h[8] == a->n_seq &&
+         h[9] == (a->k_rows != nullptr ? 1 : 0) && h[10] == g.shape && h[0] >= 0 && h[0] <= z.items && h[4] >= 0 &&
+         h[4] <= z.merges && h[6] == kPlanHeader + kMergeInts * h[4] && h[7] >= 0 && h[7] <= split_slots(g) &&
+         (h[4] == 0) == (h[7] == 0);
 }
 
 int check_stride(int64_t s) { return s >= 0 && s % 8 == 0; }
+
+// The running maximum m (log2 units) is raised only when a step's maximum exceeds it by more than this, so O is
+// rescaled on few steps and P = 2^(x - m) stays below 2^8. The key that sets a row's maximum then carries a P above 1,
+// rounded to bf16 like every other P: harmless where the softmax is flat, but where one key dominates its weight's
+// rounding moves the output by up to ~2^-9 of its spread. A logit scale of order one (Gemma's unit scale on normed
+// queries and keys: logits of standard deviation ~sqrt(D)) is that regime; there the maximum is kept exact (P of
+// the dominant key exactly 1), at the cost of a rescale on every step whose maximum grows.
+float rescale_threshold(float scale) { return fabsf(scale) >= 0.5f ? 0.f : 8.f; }
 
 bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
 
@@ -71,7 +76,7 @@ int check_norm_rope(int norm, const void* weight, const void* cos, const void* s
 
 }  // namespace
 
-extern "C" int karpo_attn_version(void) { return 2; }
+extern "C" int karpo_attn_version(void) { return 3; }
 
 extern "C" const char* karpo_attn_strerror(int status) {
   switch (status) {
@@ -92,17 +97,21 @@ extern "C" const char* karpo_attn_strerror(int status) {
     case KARPO_ATTN_ERR_PROLOGUE:
       return "unsupported fused prologue / gate: norm mode 0-3 with a 16-byte aligned weight for modes 1-2, both rope "
              "tables 16-byte aligned with a row stride that is a multiple of 8, rope_dim a multiple of 32 up to "
-             "head_dim, gate strides multiples of 4";
+             "head_dim, gate strides multiples of 4, q_out only with a prologue";
+    case KARPO_ATTN_ERR_PLAN:
+      return "the plan was made for another call (tile geometry, row-table use, sequence count or sizes differ), or "
+             "its host header copy is missing";
     default: return "unknown karpo_attn status";
   }
 }
 
 extern "C" int karpo_attn_tile_shape(int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t max_q,
-                                     int32_t* rows_per_tile, int32_t* keys_per_step, int32_t* heads_per_item) {
+                                     int32_t gather, int32_t* rows_per_tile, int32_t* keys_per_step,
+                                     int32_t* heads_per_item) {
   if (heads < 1 || kv_heads < 1 || heads % kv_heads != 0) return KARPO_ATTN_ERR_HEADS;
   if (!head_dim_supported(head_dim)) return KARPO_ATTN_ERR_HEAD_DIM;
   if (max_q < 0) return KARPO_ATTN_ERR_ARG;
-  const Geometry g = geometry(heads, kv_heads, head_dim, max_q);
+  const Geometry g = geometry(heads, kv_heads, head_dim, max_q, gather != 0);
   if (rows_per_tile) *rows_per_tile = g.rows;
   if (keys_per_step) *keys_per_step = g.bn;
   if (heads_per_item) *heads_per_item = g.ng;
@@ -113,7 +122,7 @@ extern "C" int karpo_attn_plan_capacity(const KarpoAttnArgs* a, int64_t* entries
   const int st = check_shape(a);
   if (st != KARPO_ATTN_OK) return st;
   if (entries == nullptr) return KARPO_ATTN_ERR_NULL;
-  *entries = sizes_of(a, geometry(a->heads, a->kv_heads, a->head_dim, a->max_q)).plan_entries;
+  *entries = sizes_of(a, fwd_geometry(a)).plan_entries;
   return KARPO_ATTN_OK;
 }
 
@@ -121,7 +130,7 @@ extern "C" int karpo_attn_workspace_bytes(const KarpoAttnArgs* a, size_t* bytes)
   const int st = check_shape(a);
   if (st != KARPO_ATTN_OK) return st;
   if (bytes == nullptr) return KARPO_ATTN_ERR_NULL;
-  *bytes = (size_t)sizes_of(a, geometry(a->heads, a->kv_heads, a->head_dim, a->max_q)).bytes;
+  *bytes = (size_t)sizes_of(a, fwd_geometry(a)).bytes;
   return KARPO_ATTN_OK;
 }
 
@@ -145,8 +154,11 @@ extern "C" int karpo_attn_fwd(const KarpoAttnArgs* a, void* stream) {
     return KARPO_ATTN_ERR_PROLOGUE;
   if (a->lse != nullptr && (a->gate != nullptr || (reinterpret_cast<uintptr_t>(a->lse) & 3u) != 0))
     return KARPO_ATTN_ERR_ARG;
+  if (a->q_out != nullptr && ((a->q_norm == KARPO_NORM_NONE && a->rope_cos == nullptr) || !aligned16(a->q_out) ||
+                              !check_stride(a->q_out_stride_tok) || !check_stride(a->q_out_stride_head)))
+    return KARPO_ATTN_ERR_PROLOGUE;
 
-  const Geometry g = geometry(a->heads, a->kv_heads, a->head_dim, a->max_q);
+  const Geometry g = fwd_geometry(a);
   // a step's key rows are addressed with 32-bit byte offsets
   if ((a->k_stride_tok + a->head_dim) * g.bn * 2 >= (int64_t)INT32_MAX ||
       (a->v_stride_tok + a->head_dim) * g.bn * 2 >= (int64_t)INT32_MAX)
@@ -157,10 +169,12 @@ extern "C" int karpo_attn_fwd(const KarpoAttnArgs* a, void* stream) {
     const int64_t vspan = (a->total_k - 1) * a->v_stride_tok + a->head_dim;
     if (kspan * 2 >= (int64_t)UINT32_MAX - 16 || vspan * 2 >= (int64_t)UINT32_MAX - 16) return KARPO_ATTN_ERR_LAYOUT;
   }
-  const Sizes z = sizes_of(a, g);
+  const FwdSizes z = sizes_of(a, g);
   if (z.plan_entries > (int64_t)INT32_MAX / 2 || z.items * g.n_hg > (int64_t)INT32_MAX) return KARPO_ATTN_ERR_ARG;
+  if (a->plan != nullptr && (a->plan_header == nullptr || !plan_matches(a->plan_header, a, g, z)))
+    return KARPO_ATTN_ERR_PLAN;
   // a host plan that splits no tile needs neither the planner's space nor partials
-  const bool merge = split_slots(g) >= 2 && !(a->plan != nullptr && a->plan_unsplit != 0);
+  const bool merge = split_slots(g) >= 2 && !(a->plan != nullptr && a->plan_header[4] == 0);
   if ((a->plan == nullptr || merge) &&
       (a->workspace == nullptr || a->workspace_bytes < (size_t)z.bytes || !aligned16(a->workspace)))
     return KARPO_ATTN_ERR_WORKSPACE;
@@ -170,8 +184,9 @@ extern "C" int karpo_attn_fwd(const KarpoAttnArgs* a, void* stream) {
   const int32_t* plan = a->plan;
   if (plan == nullptr) {
     int32_t* dplan = reinterpret_cast<int32_t*>(ws);
-    const PlanJob job = {a->q_cu, a->k_cu, g, a->window_left, a->window_right, dplan, (int)z.tiles, (int)z.merges,
-                         (int)z.items, dplan + z.plan_entries};
+    const PlanJob job = {a->q_cu,        a->k_cu,       g,          a->window_left, a->window_right,
+                         dplan,          (int)z.tiles,  (int)z.merges, (int)z.items, dplan + z.plan_entries,
+                         dplan + z.status_offset, a->total_q, a->max_q, a->k_rows != nullptr};
     if (launch_plan(&job, 1, a->n_seq, s) != hipSuccess) return KARPO_ATTN_ERR_LAUNCH;
     plan = dplan;
   }
@@ -212,6 +227,7 @@ extern "C" int karpo_attn_fwd(const KarpoAttnArgs* a, void* stream) {
   float c = fabsf(a->scale) * 1.4426950408889634f;
   p.c = c > 1e-30f ? c : 1e-30f;
   p.qsign = a->scale < 0.f ? 0x80008000u : 0u;
+  p.tau = rescale_threshold(a->scale);
   p.q_norm = a->q_norm;
   p.q_eps = a->q_norm_eps;
   // without a weight the kernel still reads (and multiplies by zero) head_dim elements: q's first row stands in
@@ -225,7 +241,24 @@ extern "C" int karpo_attn_fwd(const KarpoAttnArgs* a, void* stream) {
   p.sg_h = a->gate_stride_head;
   p.lse = a->lse;
   p.lse_stride = a->total_q;
+  p.q_out = static_cast<uint16_t*>(a->q_out);
+  p.sqo_t = a->q_out_stride_tok;
+  p.sqo_h = a->q_out_stride_head;
   if (launch_forward(p, a->head_dim, g, z.items, merge ? z.merges : 0, s) != hipSuccess)
+    return KARPO_ATTN_ERR_LAUNCH;
+  return KARPO_ATTN_OK;
+}
+
+extern "C" int karpo_attn_device_status(const KarpoAttnArgs* a, void* stream, int32_t* status) {
+  const int st = check_shape(a);
+  if (st != KARPO_ATTN_OK) return st;
+  if (status == nullptr || a->workspace == nullptr) return KARPO_ATTN_ERR_NULL;
+  const FwdSizes z = sizes_of(a, fwd_geometry(a));
+  if (a->workspace_bytes < (size_t)z.bytes) return KARPO_ATTN_ERR_WORKSPACE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int32_t* word = static_cast<const int32_t*>(a->workspace) + z.status_offset;
+  if (hipMemcpyAsync(status, word, sizeof(int32_t), hipMemcpyDeviceToHost, s) != hipSuccess ||
+      hipStreamSynchronize(s) != hipSuccess)
     return KARPO_ATTN_ERR_LAUNCH;
   return KARPO_ATTN_OK;
 }

@@ -29,6 +29,7 @@ struct Params {
   int32_t n_hg;     // work items per tile
   int32_t left, right;
   float c;          // |scale| * log2(e)
+  float tau;        // lazy-rescale threshold in log2 units (0: the running maximum is always exact)
   uint32_t qsign;   // 0x80008000 to negate Q (negative scale), else 0
   // fused query prologue (norm, rotation) and output gate; see KarpoAttnArgs
   const uint16_t* __restrict__ q_norm_w;
@@ -41,6 +42,8 @@ struct Params {
   int32_t rope_dim;
   float* __restrict__ lse;  // [heads][lse_stride] natural-log sums, or null
   int64_t lse_stride;       // total_q
+  uint16_t* __restrict__ q_out;  // the query after the fused prologue, or null
+  int64_t sqo_t, sqo_h;
 };
 
 // The backward kernels' arguments (karpo_attn_bwd): the forward's tensors and bounds, the output gradient and the
@@ -96,7 +99,10 @@ hipError_t launch_forward_128(const Params& p, int shape, int64_t items, int64_t
                               hipStream_t stream);
 
 // One work list for the device planner: from the bounds into `plan` (room for `merges` split tiles and `items`
-// items; at most `tiles` tiles are planned), with `tile_base` (n_seq + 1 ints) as its scratch.
+// items; at most `tiles` tiles are planned), with `tile_base` (n_seq + 1 ints) as its scratch. With a `status` word
+// the planner first checks the bounds against the call's contract (non-decreasing from 0, query rows within
+// total_q, every query run at most max_q): bounds that break it get an empty plan and KARPO_ATTN_ERR_BOUNDS in
+// `status` (else KARPO_ATTN_OK), so no kernel reads or writes a row through them.
 struct PlanJob {
   const int32_t* q_cu;
   const int32_t* k_cu;
@@ -105,6 +111,10 @@ struct PlanJob {
   int32_t* plan;
   int tiles, merges, items;
   int32_t* tile_base;
+  int32_t* status;   // or null: no bounds check (the backward's work lists)
+  int64_t total_q;
+  int32_t max_q;
+  int32_t gather;    // the plan header's row-table flag
 };
 // The device planner: one workgroup per job (one or two), one launch.
 hipError_t launch_plan(const PlanJob* jobs, int n_jobs, int n_seq, hipStream_t stream);

@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "tile_addr.h"
+
 namespace karpo {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -56,22 +58,6 @@ __device__ __forceinline__ int wave_max(int x) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) x = max(x, __shfl_xor(x, o));
   return x;
-}
-
-// Where lane `lane` of DMA instruction `blk` (1 KiB of the tile each) reads: the key row inside the step and the
-// element column. Inverse of k_offset / v_offset for byte offset blk * 1024 + lane * 16.
-template <int D>
-__device__ __forceinline__ void k_dma_source(int blk, int lane, int* key, int* col) {
-  const int b = blk * 4 + (lane >> 4);  // 256-byte block: (key block, chunk)
-  *key = (b / (D / 8)) * 16 + (lane & 15);
-  *col = (b % (D / 8)) * 8;
-}
-template <int D>
-__device__ __forceinline__ void v_dma_source(int blk, int lane, int* key, int* col) {
-  const int b = blk * 8 + (lane >> 3);  // 128-byte block: (key group, d block)
-  const int piece = lane & 7;
-  *key = (b / (D / 16)) * 4 + (piece >> 1);
-  *col = (b % (D / 16)) * 16 + (piece & 1) * 8;
 }
 
 // The S layout: rows (keys, or query rows) staged once and read both as MFMA row operands (ds_read_b128, one row's

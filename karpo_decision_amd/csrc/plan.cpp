@@ -28,8 +28,11 @@ extern "C" int karpo_attn_plan(const KarpoAttnArgs* a, const int32_t* q_cu, cons
   if (capacity < kPlanHeader) return KARPO_ATTN_ERR_CAPACITY;
   for (int32_t i = 0; i < n_seq; ++i)
     if (q_cu[i] < 0 || k_cu[i] < 0 || q_cu[i + 1] < q_cu[i] || k_cu[i + 1] < k_cu[i]) return KARPO_ATTN_ERR_BOUNDS;
+  for (int32_t i = 0; i < n_seq; ++i)  // max_q bounds every query run (it sizes the tiles and the launch)
+    if (q_cu[i + 1] - q_cu[i] > a->max_q) return KARPO_ATTN_ERR_BOUNDS;
 
-  const Geometry g = geometry(a->heads, a->kv_heads, a->head_dim, a->max_q);
+  const bool gather = a->k_rows != nullptr;  // calls through a row table take their own tile shape
+  const Geometry g = geometry(a->heads, a->kv_heads, a->head_dim, a->max_q, gather);
   struct Tile {
     int32_t seg, tile;
     int64_t steps;
@@ -75,6 +78,10 @@ extern "C" int karpo_attn_plan(const KarpoAttnArgs* a, const int32_t* q_cu, cons
   plan[5] = g.waves;
   plan[6] = (int32_t)first;
   plan[7] = slots;
+  plan[8] = n_seq;
+  plan[9] = gather ? 1 : 0;
+  plan[10] = g.shape;
+  plan[11] = 0;
   std::copy(merges.begin(), merges.end(), plan + kPlanHeader);
   for (size_t n = 0; n < items.size(); ++n) {
     int32_t* e = plan + first + kItemInts * n;

@@ -58,7 +58,7 @@ KA_HD constexpr int tiles_per_cu(int head_dim, int shape) {
   return shape == kNarrow ? (head_dim == 512 ? 1 : 2) : head_dim == 64 ? 4 : 1;
 }
 constexpr int kComputeUnits = 256;   // MI355X
-constexpr int kPlanHeader = 8;       // int32 header of a plan (see karpo_attn.h)
+constexpr int kPlanHeader = 12;      // int32 header of a plan (see karpo_attn.h)
 constexpr int kItemInts = 4;         // per work item: segment, tile, part | parts << 16, first partial slot or -1
 constexpr int kMergeInts = 4;        // per split tile: segment, tile, parts, first partial slot
 constexpr int kCostBuckets = 2048;   // device planner's cost histogram (costs clamp to the last bucket)
@@ -92,15 +92,28 @@ KA_HD inline Geometry geometry_of(int heads, int kv_heads, int head_dim, int sha
 }
 
 // The tile shape for a pack whose longest query run is max_q: narrow when every sequence's queries fit one narrow
-// tile; small for short runs at head_dim 128 and 256; long for very long runs at 128; else wide.
-KA_HD inline int tile_shape(int heads, int kv_heads, int head_dim, int64_t max_q) {
+// tile; small for short runs at head_dim 128 and 256; long for very long runs at 128; else wide. Calls that read
+// their keys through a row table (`gather`) take the small tiles at head_dim 128 and 256 whatever the run: the wide
+// and long tiles are not built with a row table (their copies leave some waves without a copy instruction, a
+// configuration whose only run through a row table ended in a GPU memory fault that no host replay of its
+// addresses reproduces), and the small tiles are the faster shape on block plans' branched packs anyway.
+KA_HD inline int tile_shape(int heads, int kv_heads, int head_dim, int64_t max_q, bool gather = false) {
   if (max_q <= geometry_of(heads, kv_heads, head_dim, kNarrow).rows) return kNarrow;
-  if ((head_dim == 128 && max_q <= 4096) || (head_dim == 256 && max_q <= 8192)) return kSmall;
+  if (head_dim == 128 || head_dim == 256) {
+    if (gather || (head_dim == 128 && max_q <= 4096) || (head_dim == 256 && max_q <= 8192)) return kSmall;
+  }
   if (head_dim == 128 && max_q > 65536) return kLong;
   return kWide;
 }
-KA_HD inline Geometry geometry(int heads, int kv_heads, int head_dim, int64_t max_q) {
-  return geometry_of(heads, kv_heads, head_dim, tile_shape(heads, kv_heads, head_dim, max_q));
+KA_HD inline Geometry geometry(int heads, int kv_heads, int head_dim, int64_t max_q, bool gather = false) {
+  return geometry_of(heads, kv_heads, head_dim, tile_shape(heads, kv_heads, head_dim, max_q, gather));
+}
+
+// K/V buffers of the forward kernel's ring (steps of copies in flight: buffers - 1). One-wave tiles that stream
+// their keys without a row table (decode-shaped packs, HBM bound) keep three steps in flight at head_dim 64 and 128
+// (four buffers); every other tile double-buffers.
+KA_HD constexpr int kv_buffers(int head_dim, int shape, bool gather) {
+  return shape == kNarrow && tile_waves(head_dim, shape) == 1 && !gather && head_dim <= 128 ? 4 : 2;
 }
 
 KA_HD inline int64_t ka_min(int64_t a, int64_t b) { return a < b ? a : b; }
@@ -142,6 +155,36 @@ KA_HD inline int part_cost(int64_t steps, int parts) {
 // Partial slots (per head group) the parts of split tiles can take, and the split tiles there can be.
 KA_HD inline int64_t split_slots(const Geometry& g) { return 2 * (int64_t)g.conc / g.n_hg; }
 KA_HD inline int64_t split_tiles(const Geometry& g) { return split_slots(g) / 2; }
+
+// Tiles a forward launch covers at most: every sequence adds at most one partial tile, and none has more than max_q
+// rows (rows: the query rows the bounds span, at most total_q).
+KA_HD inline int64_t tile_capacity(int64_t total_q, int n_seq, int64_t max_q, const Geometry& g) {
+  const int64_t by_rows = (total_q + g.rows - 1) / g.rows + n_seq;
+  const int64_t by_max = (int64_t)n_seq * tiles_of(max_q, g.rows);
+  return by_rows < by_max ? by_rows : by_max;
+}
+
+// Sizes of one forward call's plan and workspace. Items: every unsplit tile once plus the parts of split tiles (at
+// most split_slots); split tiles: at most half the slots. (Bound: with `total` the pack's workgroup-steps and
+// tau >= total / conc, a tile of s > tau steps splits into ceil(s / tau) < 2 s / tau parts, so the parts of all split
+// tiles number below 2 total / (tau n_hg) <= 2 conc / n_hg, an integer bound of split_slots.) The workspace holds
+// the device plan, the planner's tile bases (n_seq + 1), its status word, then the fp32 partials.
+struct FwdSizes {
+  int64_t tiles, items, merges, plan_entries, status_offset, partial_offset, bytes;
+};
+KA_HD inline FwdSizes fwd_sizes(int64_t total_q, int n_seq, int64_t max_q, int head_dim, const Geometry& g) {
+  FwdSizes z;
+  z.tiles = tile_capacity(total_q, n_seq, max_q, g);
+  z.items = z.tiles + split_slots(g);
+  z.merges = ka_min(z.tiles, split_tiles(g));
+  z.plan_entries = kPlanHeader + kMergeInts * z.merges + kItemInts * z.items;
+  z.status_offset = z.plan_entries + (int64_t)n_seq + 1;  // int offset: after the plan and the tile bases
+  const int64_t ints = z.status_offset + 1;
+  z.partial_offset = (ints * 4 + 255) / 256 * 256;
+  const int64_t partial = split_slots(g) * g.n_hg * (int64_t)g.vectors * (head_dim + 2) * 4;
+  z.bytes = z.partial_offset + (partial + 255) / 256 * 256;
+  return z;
+}
 
 // Backward tiles (attn_bwd.hip), never split (conc 1 makes the split length the whole pack):
 //   * dkdv kernel: four waves of 32 keys, 32 query rows per step;

@@ -96,7 +96,7 @@ def check_inputs(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_cu: 
 
 def _args(query: Tensor, key: Tensor, value: Tensor, out: Tensor | None, q_cu: Tensor | None, k_cu: Tensor | None,
           n_seq: int, max_q: int, scale: float, window_left: int, window_right: int, spans: Tensor | None,
-          plan: Tensor | None, plan_split_tiles: int = -1, key_rows: Tensor | None = None, q_norm: int = 0,
+          plan: Tensor | None, plan_header: list[int] | None = None, key_rows: Tensor | None = None, q_norm: int = 0,
           q_norm_eps: float = 0.0, q_norm_weight: Tensor | None = None, rope_cos: Tensor | None = None,
           rope_sin: Tensor | None = None, gate: Tensor | None = None) -> _lib.KarpoAttnArgs:
     a = _lib.KarpoAttnArgs()
@@ -117,7 +117,8 @@ def _args(query: Tensor, key: Tensor, value: Tensor, out: Tensor | None, q_cu: T
     if spans is not None and spans.numel():
         a.spans, a.n_spans = spans.data_ptr(), spans.shape[0]
     a.plan = plan.data_ptr() if plan is not None else 0
-    a.plan_unsplit = 1 if plan is not None and plan_split_tiles == 0 else 0
+    if plan_header is not None:  # the struct keeps the array alive (ctypes holds assigned objects)
+        a.plan_header = (ctypes.c_int32 * len(plan_header))(*plan_header)
     if key_rows is not None:
         a.k_rows, a.total_k = key_rows.data_ptr(), key.shape[0]
     a.q_norm, a.q_norm_eps = q_norm, q_norm_eps
@@ -133,19 +134,30 @@ def _args(query: Tensor, key: Tensor, value: Tensor, out: Tensor | None, q_cu: T
 
 def _packed_attention(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_cu: Tensor, max_q: int,
                      scale: float, window_left: int, window_right: int, spans: Tensor | None,
-                     plan: Tensor | None, plan_split_tiles: int = -1, key_rows: Tensor | None = None,
+                     plan: Tensor | None, plan_header: list[int] | None = None, key_rows: Tensor | None = None,
                      q_norm: int = 0, q_norm_eps: float = 0.0, q_norm_weight: Tensor | None = None,
                      rope_cos: Tensor | None = None, rope_sin: Tensor | None = None,
                      gate: Tensor | None = None) -> Tensor:
+    return _attention_impl(query, key, value, q_cu, k_cu, max_q, scale, window_left, window_right, spans, plan,
+                           plan_header, key_rows, q_norm, q_norm_eps, q_norm_weight, rope_cos, rope_sin, gate)
+
+
+def _attention_impl(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_cu: Tensor, max_q: int,
+                    scale: float, window_left: int, window_right: int, spans: Tensor | None,
+                    plan: Tensor | None, plan_header: list[int] | None = None, key_rows: Tensor | None = None,
+                    q_norm: int = 0, q_norm_eps: float = 0.0, q_norm_weight: Tensor | None = None,
+                    rope_cos: Tensor | None = None, rope_sin: Tensor | None = None,
+                    gate: Tensor | None = None, query_out: Tensor | None = None) -> Tensor:
     """(Tq, heads, D) bf16: sequence i's query rows q_cu[i]:q_cu[i+1] over its key rows k_cu[i]:k_cu[i+1] (bounds
     int32 on the device), query i at key coordinate i + Lk - Lq, seeing keys j with i' - left <= j <= i' + right
     (-1: unbounded), or in its own span (``spans`` (n, 2) int32 query-row ranges); ``plan`` a device work list from
-    ``make_plan`` or None (planned on the device), ``plan_split_tiles`` its split-tile count when known (-1);
+    ``make_plan`` or None (planned on the device), ``plan_header`` its host header (required with ``plan``);
     ``key_rows`` (int32 on the device) maps key row r to row key_rows[r] of ``key`` / ``value`` (a gather read in
     place, as ``key.index_select(0, key_rows)`` would give). Fused prologue: ``query`` is the projection's output,
     normalised (``q_norm`` NORM_*, ``q_norm_weight`` bf16 (D,), ``q_norm_eps``) and rotated by halves over the first
     ``rope_cos.shape[-1]`` elements (``rope_cos`` / ``rope_sin`` bf16 (Tq, R), row i for query row i) as the kernel
-    loads it; fused epilogue: the output times sigmoid(``gate``) (bf16, the output's shape)."""
+    loads it; fused epilogue: the output times sigmoid(``gate``) (bf16, the output's shape). ``query_out`` (bf16, the
+    query's shape; eager calls only) receives the query after the prologue, the attention's actual query."""
     check_inputs(query, key, value, q_cu, k_cu)
     if query.device.type != "cuda":
         raise ValueError(f"packed attention runs on an MI355X GPU, not on {query.device}")
@@ -169,6 +181,10 @@ def _packed_attention(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k
     if rope_cos is not None and (rope_sin is None or rope_cos.shape != rope_sin.shape or rope_cos.dim() != 2
                                  or rope_cos.shape[0] < query.shape[0]):
         raise ValueError("rope_cos and rope_sin must be (query rows, rotated elements) tables of one shape")
+    if query_out is not None and (query_out.shape != query.shape or query_out.dtype != torch.bfloat16
+                                  or query_out.device != query.device or query_out.stride(2) != 1
+                                  or (q_norm == NORM_NONE and rope_cos is None)):
+        raise ValueError("query_out must be a bf16 tensor of the query's shape, with a fused prologue")
     lib = _lib.load()
     out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
     if query.shape[0] == 0:
@@ -176,10 +192,13 @@ def _packed_attention(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k
     q_cu, k_cu = q_cu.contiguous(), k_cu.contiguous()
     with torch.cuda.device(query.device):
         args = _args(query, key, value, out, q_cu, k_cu, q_cu.numel() - 1, max_q, scale, window_left, window_right,
-                     spans, plan, plan_split_tiles, key_rows, q_norm, q_norm_eps, q_norm_weight, rope_cos, rope_sin,
+                     spans, plan, plan_header, key_rows, q_norm, q_norm_eps, q_norm_weight, rope_cos, rope_sin,
                      gate)
+        if query_out is not None:
+            args.q_out = query_out.data_ptr()
+            args.q_out_stride_tok, args.q_out_stride_head = query_out.stride(0), query_out.stride(1)
         workspace = None
-        if not args.plan_unsplit:
+        if plan is None or plan_header is None or plan_header[4] != 0:  # a plan that splits nothing needs none
             need = ctypes.c_size_t()
             _lib.check(lib.karpo_attn_workspace_bytes(ctypes.byref(args), ctypes.byref(need)), "packed attention")
             # the device plan and the fp32 partials of split tiles, from the caching allocator (stream-ordered reuse)
@@ -196,7 +215,7 @@ packed_attention = torch.library.custom_op(f"{NAMESPACE}::packed_attention", mut
 
 
 @packed_attention.register_fake
-def _(query, key, value, q_cu, k_cu, max_q, scale, window_left, window_right, spans, plan, plan_split_tiles=-1,
+def _(query, key, value, q_cu, k_cu, max_q, scale, window_left, window_right, spans, plan, plan_header=None,
       key_rows=None, q_norm=0, q_norm_eps=0.0, q_norm_weight=None, rope_cos=None, rope_sin=None, gate=None):
     return query.new_empty(query.shape)
 
@@ -204,31 +223,41 @@ def _(query, key, value, q_cu, k_cu, max_q, scale, window_left, window_right, sp
 @dataclass(frozen=True)
 class Plan:
     """A pack's work list on the device, built once on the host (like ``block_plan``'s bounds,
-    families/gemma/packed.py:103-151) and reused by every layer of the same head geometry, window and tile shape."""
+    families/gemma/packed.py:103-151) and reused by every layer of the same head geometry, window, tile shape and
+    row-table use; ``header`` is its host copy of the plan's header (the C ABI checks it against each call)."""
 
     tensor: Tensor
+    header: tuple[int, ...]
     heads: int
     kv_heads: int
     head_dim: int
     window_left: int
     window_right: int
     max_q: int
-    items: int
-    rows_per_tile: int
-    split_tiles: int
+    n_seq: int
+    gather: bool
     query_end: int = 0  # q_cu[-1] and k_cu[-1]: the rows the bounds index (checked against the tensors in ``run``)
     key_end: int = 0
 
     @property
-    def header(self) -> list[int]:
-        return self.tensor[:8].tolist()
+    def items(self) -> int:
+        return self.header[0]
+
+    @property
+    def rows_per_tile(self) -> int:
+        return self.header[1]
+
+    @property
+    def split_tiles(self) -> int:
+        return self.header[4]
 
 
 def make_plan(q_cu: list[int] | Tensor, k_cu: list[int] | Tensor, heads: int, kv_heads: int, head_dim: int,
               window_left: int = -1, window_right: int = -1, device: torch.device | str = "cuda",
-              max_q: int | None = None) -> Plan:
+              max_q: int | None = None, gather: bool = False) -> Plan:
     """The longest-first work list for host bounds ``q_cu`` / ``k_cu`` (lists or CPU tensors), on ``device``.
-    ``max_q`` (default: the longest query run) must be the value the calls pass: it selects the tile shape."""
+    ``max_q`` (default: the longest query run) must be the value the calls pass: it selects the tile shape;
+    ``gather``: the calls read their keys through a row table (``key_rows``), which selects the tile shape too."""
     qc = [int(x) for x in (q_cu.tolist() if isinstance(q_cu, Tensor) else q_cu)]
     kc = [int(x) for x in (k_cu.tolist() if isinstance(k_cu, Tensor) else k_cu)]
     if len(qc) != len(kc) or not qc:
@@ -244,6 +273,9 @@ def make_plan(q_cu: list[int] | Tensor, k_cu: list[int] | Tensor, heads: int, kv
     a.heads, a.kv_heads, a.head_dim = heads, kv_heads, head_dim
     a.window_left, a.window_right = window_left, window_right
     a.n_seq, a.total_q, a.max_q = n, qc[-1] - qc[0], max_q
+    marker = ctypes.c_int32()  # karpo_attn_plan reads only whether k_rows is set
+    if gather:
+        a.k_rows = ctypes.addressof(marker)
     entries = ctypes.c_int64()
     _lib.check(lib.karpo_attn_plan_capacity(ctypes.byref(a), ctypes.byref(entries)), "karpo_attn_plan_capacity")
     qa = (ctypes.c_int32 * len(qc))(*qc)
@@ -252,8 +284,8 @@ def make_plan(q_cu: list[int] | Tensor, k_cu: list[int] | Tensor, heads: int, kv
     _lib.check(lib.karpo_attn_plan(ctypes.byref(a), qa, ka, n, buf, entries.value), "karpo_attn_plan")
     used = buf[6] + 4 * buf[0]
     host = torch.tensor(list(buf[:used]), dtype=torch.int32)
-    return Plan(host.to(device), heads, kv_heads, head_dim, window_left, window_right, max_q, int(buf[0]),
-                int(buf[1]), int(buf[4]), qc[-1], kc[-1])
+    return Plan(host.to(device), tuple(buf[:_lib.PLAN_HEADER]), heads, kv_heads, head_dim, window_left, window_right,
+                max_q, n, bool(gather), qc[-1], kc[-1])
 
 
 def key_rows_of(rows: Tensor | None) -> Tensor | None:
@@ -266,17 +298,26 @@ def key_rows_of(rows: Tensor | None) -> Tensor | None:
 def run(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_cu: Tensor, max_q: int, scale: float,
         window_left: int = -1, window_right: int = -1, spans: Tensor | None = None,
         plan: Plan | None = None, key_rows: Tensor | None = None, q_norm: Norm | None = None,
-        rope: tuple[Tensor, Tensor] | None = None, gate: Tensor | None = None) -> Tensor:
+        rope: tuple[Tensor, Tensor] | None = None, gate: Tensor | None = None,
+        query_out: Tensor | None = None) -> Tensor:
     """``packed_attention`` with a ``Plan`` checked against the call's geometry; ``key_rows`` (int32 or int64) reads
     the keys and values through a row table instead of a gathered copy; ``q_norm`` / ``rope`` ((cos, sin), (rows, R)
-    or (1, rows, R)) the fused query prologue, ``gate`` the fused sigmoid gate on the output."""
-    tensor, split_tiles = None, -1
+    or (1, rows, R)) the fused query prologue, ``gate`` the fused sigmoid gate on the output; ``query_out`` receives
+    the query after the prologue (eager calls only: torch.compile sees an operator without it)."""
+    tensor, header = None, None
     if plan is not None:
         if (plan.heads, plan.kv_heads, plan.head_dim, plan.window_left, plan.window_right) != (
                 query.shape[1], key.shape[1], query.shape[2], window_left, window_right):
             raise ValueError("the plan was made for another head geometry or window")
-        if _lib.tile_shape(plan.heads, plan.kv_heads, plan.head_dim, plan.max_q) != _lib.tile_shape(
-                plan.heads, plan.kv_heads, plan.head_dim, int(max_q)):
+        if plan.n_seq != q_cu.numel() - 1:
+            raise ValueError(f"the plan was made for {plan.n_seq} sequences, the call has {q_cu.numel() - 1}")
+        if plan.gather != (key_rows is not None):
+            raise ValueError("the plan was made " + ("with" if plan.gather else "without") + " a row table, the call "
+                             + ("has none" if plan.gather else "reads its keys through one"))
+        if int(max_q) < plan.max_q:
+            raise ValueError(f"max_q {max_q} is below the plan's {plan.max_q}: it must bound every query run")
+        if _lib.tile_shape(plan.heads, plan.kv_heads, plan.head_dim, plan.max_q, plan.gather) != _lib.tile_shape(
+                plan.heads, plan.kv_heads, plan.head_dim, int(max_q), plan.gather):
             raise ValueError(f"the plan was made for max_q {plan.max_q}, another tile shape than max_q {max_q}")
         # the plan's host bounds: rows past the tensors would be read out of their allocations
         if plan.query_end > query.shape[0]:
@@ -285,7 +326,7 @@ def run(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_cu: Tensor, m
         if plan.key_end > key_rows_len:
             raise ValueError(f"the bounds index {plan.key_end} key rows, the {'key' if key_rows is None else 'row table'}"
                              f" has {key_rows_len}")
-        tensor, split_tiles = plan.tensor, plan.split_tiles
+        tensor, header = plan.tensor, list(plan.header)
     mode, eps, weight = NORM_NONE, 0.0, None
     if q_norm is not None:
         mode, eps = int(q_norm.mode), float(q_norm.eps)
@@ -297,9 +338,13 @@ def run(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_cu: Tensor, m
     # one is torch's error, not a silently detached output); the implementation itself otherwise
     traced = torch.compiler.is_compiling() or (torch.is_grad_enabled() and (
         query.requires_grad or key.requires_grad or value.requires_grad))
-    op = packed_attention if traced else _packed_attention
-    return op(query, key, value, q_cu, k_cu, int(max_q), float(scale), int(window_left), int(window_right), spans,
-              tensor, split_tiles, key_rows_of(key_rows), mode, eps, weight, cos, sin, gate)
+    call = (query, key, value, q_cu, k_cu, int(max_q), float(scale), int(window_left), int(window_right), spans,
+            tensor, header, key_rows_of(key_rows), mode, eps, weight, cos, sin, gate)
+    if query_out is not None:
+        if traced:
+            raise RuntimeError("query_out is written by eager calls only (the registered operator has no such output)")
+        return _attention_impl(*call, query_out=query_out)
+    return (packed_attention if traced else _packed_attention)(*call)
 
 
 def norm_rope(x: Tensor, norm: Norm | None, rope: tuple[Tensor, Tensor] | None = None,
@@ -309,10 +354,21 @@ def norm_rope(x: Tensor, norm: Norm | None, rope: tuple[Tensor, Tensor] | None =
     may be ``x`` (in place); a new tensor otherwise."""
     if x.dim() != 3 or x.dtype != torch.bfloat16 or x.device.type != "cuda":
         raise ValueError("norm_rope takes a (rows, heads, head_dim) bf16 tensor on the GPU")
+    if x.shape[2] not in (64, 128, 256, 512) or x.stride(2) != 1:
+        raise ValueError(f"norm_rope takes head_dim 64, 128, 256 or 512 with a contiguous head, not {tuple(x.shape)}")
     if out is None:
         out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
-    elif out.shape != x.shape or out.dtype != x.dtype:
-        raise ValueError("out must have x's shape and dtype")
+    elif out.shape != x.shape or out.dtype != x.dtype or out.device != x.device or out.stride(2) != 1:
+        raise ValueError("out must have x's shape, dtype and device, with a contiguous head")
+    if norm is not None and norm.mode in (NORM_WEIGHT, NORM_ONE_PLUS) and (
+            norm.weight is None or tuple(norm.weight.shape) != (x.shape[2],)):
+        raise ValueError(f"the norm's weight must have shape ({x.shape[2]},)")
+    if rope is not None:
+        cos, sin = rope
+        cos, sin = (t[0] if t.dim() == 3 and t.shape[0] == 1 else t for t in (cos, sin))
+        if cos.shape != sin.shape or cos.dim() != 2 or cos.shape[0] < x.shape[0] or cos.shape[1] > x.shape[2]:
+            raise ValueError(f"rope tables must be two (rows >= {x.shape[0]}, rotated <= {x.shape[2]}) tables of one "
+                             f"shape, not {tuple(cos.shape)} / {tuple(sin.shape)}")
     lib = _lib.load()
     a = _lib.KarpoNormRopeArgs()
     a.x, a.y = x.data_ptr(), out.data_ptr()

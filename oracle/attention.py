@@ -38,17 +38,20 @@ def span_ids(qa: int, lq: int, lk: int, spans: Sequence[tuple[int, int]]) -> tup
 
 
 def visible(lq: int, lk: int, left: int = -1, right: int = -1, q_span: torch.Tensor | None = None,
-            k_span: torch.Tensor | None = None) -> torch.Tensor:
-    """(lq, lk) bool: which keys each query of one sequence sees (varlen_reference's rule, OR same span)."""
-    i = torch.arange(lq)[:, None] + (lk - lq)
+            k_span: torch.Tensor | None = None, rows: torch.Tensor | None = None) -> torch.Tensor:
+    """(lq, lk) bool: which keys each query of one sequence sees (varlen_reference's rule, OR same span); with
+    ``rows`` (local query indices) only those queries' rows, (len(rows), lk)."""
+    local = torch.arange(lq) if rows is None else rows.long()
+    i = local[:, None] + (lk - lq)
     j = torch.arange(lk)[None, :]
-    ok = torch.ones(lq, lk, dtype=torch.bool)
+    ok = torch.ones(local.shape[0], lk, dtype=torch.bool)
     if right >= 0:
         ok &= j <= i + right
     if left >= 0:
         ok &= j >= i - left
     if q_span is not None and k_span is not None:
-        ok |= (q_span[:, None] == k_span[None, :]) & (q_span[:, None] >= 0)
+        qs = q_span[local]
+        ok |= (qs[:, None] == k_span[None, :]) & (qs[:, None] >= 0)
     return ok
 
 
@@ -99,7 +102,7 @@ def packed_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor
         elif window_left < 0 and window_right < 0 and not has_span:
             o = F.scaled_dot_product_attention(qs, ks, vs, scale=scale)
         else:
-            mask = visible(lq, lk, window_left, window_right, q_id, k_id)[torch.from_numpy(local)]
+            mask = visible(lq, lk, window_left, window_right, q_id, k_id, rows=torch.from_numpy(local))
             o = F.scaled_dot_product_attention(qs, ks, vs, attn_mask=mask, scale=scale)
             o = torch.where(mask.any(-1)[None, None, :, None], o, torch.zeros((), dtype=o.dtype))
         out[dest] = o[0].transpose(0, 1)

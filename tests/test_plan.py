@@ -30,7 +30,7 @@ def test_library_exports_every_declared_function():
     assert set(names) == set(_lib.EXPORTS)
     for name in names:
         assert hasattr(lib, name), name
-    assert lib.karpo_attn_version() == 2
+    assert lib.karpo_attn_version() == 3
 
 
 def host_plan(q_cu, k_cu, heads, kv_heads, head_dim, left, right, max_q=_lib.LONG):
@@ -48,8 +48,9 @@ def host_plan(q_cu, k_cu, heads, kv_heads, head_dim, left, right, max_q=_lib.LON
     st_ = lib.karpo_attn_plan(ctypes.byref(a), (ctypes.c_int32 * len(q_cu))(*q_cu),
                               (ctypes.c_int32 * len(k_cu))(*k_cu), n, buf, cap)
     _lib.check(st_, "plan")
-    header = list(buf[:8])
-    merges = [tuple(buf[8 + 4 * i: 12 + 4 * i]) for i in range(header[4])]
+    header = list(buf[:_lib.PLAN_HEADER])
+    h = _lib.PLAN_HEADER
+    merges = [tuple(buf[h + 4 * i: h + 4 + 4 * i]) for i in range(header[4])]
     slot_of = {(m[0], m[1]): m[3] for m in merges}
     items = []
     for i in range(header[0]):
@@ -101,8 +102,9 @@ def test_host_plan_matches_brute_force(q_lens, extra, geom, left, right, short):
     rows, bn, per, narrow, merges, items = expected_plan(q_cu, k_cu, heads, kv_heads, head_dim, left, right, max_q)
     header, got_merges, got_items = host_plan(q_cu, k_cu, heads, kv_heads, head_dim, left, right, max_q)
     assert header[:7] == [len(items), rows, bn, per, len(merges), waves_of(rows, per, head_dim),
-                          8 + 4 * len(merges)]
+                          _lib.PLAN_HEADER + 4 * len(merges)]
     assert header[7] == sum(m[2] for m in merges)
+    assert header[8:] == [len(q_cu) - 1, 0, _lib.kernel_shape(heads, kv_heads, head_dim, max_q), 0]
     assert got_merges == merges
     assert got_items == items
     # every part of a split tile is listed once; the slots of split tiles do not overlap
@@ -174,12 +176,16 @@ def test_tile_geometry():
 def test_plan_refuses_bad_bounds_and_small_buffers():
     lib = _lib.load()
     a = _lib.KarpoAttnArgs()
-    a.heads, a.kv_heads, a.head_dim, a.window_left, a.window_right = 4, 2, 64, -1, 0
-    buf = (ctypes.c_int32 * 8)()
+    a.heads, a.kv_heads, a.head_dim, a.window_left, a.window_right, a.max_q = 4, 2, 64, -1, 0, 1000
+    h = _lib.PLAN_HEADER
+    buf = (ctypes.c_int32 * h)()
     dec = (ctypes.c_int32 * 3)(0, 10, 5)
     inc = (ctypes.c_int32 * 3)(0, 300, 600)
-    assert lib.karpo_attn_plan(ctypes.byref(a), dec, dec, 2, buf, 8) == _lib.ERR_BOUNDS
-    assert lib.karpo_attn_plan(ctypes.byref(a), inc, inc, 2, buf, 8) == 10  # capacity
+    assert lib.karpo_attn_plan(ctypes.byref(a), dec, dec, 2, buf, h) == _lib.ERR_BOUNDS
+    assert lib.karpo_attn_plan(ctypes.byref(a), inc, inc, 2, buf, h) == 10  # capacity
+    assert lib.karpo_attn_plan(ctypes.byref(a), inc, inc, 2, buf, h - 1) == 10  # not even the header
+    a.max_q = 299  # max_q must bound every query run (it sizes the tiles and the launch)
+    assert lib.karpo_attn_plan(ctypes.byref(a), inc, inc, 2, buf, h) == _lib.ERR_BOUNDS
 
 
 def _args(**kw):
@@ -210,13 +216,74 @@ def _args(**kw):
     (dict(k_stride_tok=130), _lib.ERR_LAYOUT),
     (dict(q=0), 1),
     (dict(), 5),  # no workspace and no plan
-    (dict(plan=1 << 22), 5),  # a host plan that may split tiles needs the partials' workspace
+    (dict(plan=1 << 22), _lib.ERR_PLAN),  # a host plan without its header copy
 ])
 def test_fwd_refuses_before_launch(change, status):
     lib = _lib.load()
     a = _args(**change)
     assert lib.karpo_attn_fwd(ctypes.byref(a), None) == status
     assert _lib.message(status)
+
+
+def _header(*values):
+    return (ctypes.c_int32 * _lib.PLAN_HEADER)(*values)
+
+
+def _call_header(a, gather=False):
+    """The header karpo_attn_plan writes for the call ``a``'s geometry (one sequence of max_q rows)."""
+    lib = _lib.load()
+    b = _args(n_seq=a.n_seq, total_q=a.total_q, max_q=a.max_q)
+    marker = ctypes.c_int32()
+    if gather:
+        b.k_rows = ctypes.addressof(marker)
+    cu = (ctypes.c_int32 * 2)(0, a.max_q)
+    entries = ctypes.c_int64()
+    assert lib.karpo_attn_plan_capacity(ctypes.byref(b), ctypes.byref(entries)) == 0
+    buf = (ctypes.c_int32 * entries.value)()
+    assert lib.karpo_attn_plan(ctypes.byref(b), cu, cu, 1, buf, entries.value) == 0
+    return list(buf[:_lib.PLAN_HEADER])
+
+
+@pytest.mark.parametrize("field,value", [
+    (1, 7), (2, 16), (3, 1), (5, 8),  # another tile geometry (rows, keys per step, heads per item, waves)
+    (8, 2),  # another sequence count: the kernel would read bounds past the call's
+    (9, 1),  # made for a row table
+    (10, 2),  # another shape
+    (0, 10 ** 6),  # more items than the launch covers
+    (4, 10 ** 6),  # more split tiles than the merge launch covers
+    (7, 10 ** 6),  # more partial slots than the workspace holds
+    (6, 9),  # items not right after the split tiles
+])
+def test_fwd_refuses_a_plan_made_for_another_call(field, value):
+    """karpo_attn_fwd checks a host plan's header against the call before launching anything: a plan for another
+    geometry, row-table use, sequence count or beyond the launch's capacities would leave rows unwritten."""
+    lib = _lib.load()
+    a = _args(workspace=1 << 24, workspace_bytes=1 << 30)
+    good = _call_header(a)
+    assert good[8:11] == [1, 0, 0]
+    bad = list(good)
+    bad[field] = value
+    a.plan, a.plan_header = 1 << 22, _header(*bad)
+    assert lib.karpo_attn_fwd(ctypes.byref(a), None) == _lib.ERR_PLAN
+    # a call through a row table refuses the plan made without one, and the other way round
+    rows = _args(workspace=1 << 24, workspace_bytes=1 << 30, k_rows=1 << 22, total_k=100, plan=1 << 22)
+    rows.plan_header = _header(*good)
+    assert lib.karpo_attn_fwd(ctypes.byref(rows), None) == _lib.ERR_PLAN
+    a.plan_header = _header(*_call_header(a, gather=True))
+    assert lib.karpo_attn_fwd(ctypes.byref(a), None) == _lib.ERR_PLAN
+
+
+def test_row_table_calls_take_the_four_wave_tiles():
+    """At head sizes 128 and 256 a call through a row table takes the four-wave tiles whatever its longest run (the
+    wide and long tiles are not built with a row table); head sizes 64 and 512 keep their shapes."""
+    for max_q in (4097, 32768, 70000):
+        assert _lib.kernel_shape(32, 16, 128, max_q, gather=True) == 2
+    assert _lib.kernel_shape(16, 8, 256, 9000, gather=True) == 2
+    assert _lib.kernel_shape(32, 16, 128, 16, gather=True) == 1  # one-wave tiles stay
+    assert _lib.kernel_shape(8, 2, 64, 5000, gather=True) == 0
+    assert _lib.kernel_shape(32, 4, 512, 5000, gather=True) == 0
+    plan = ops.make_plan([0, 5000], [0, 5000], 32, 16, 128, -1, 0, device="cpu", gather=True)
+    assert plan.gather and plan.header[9] == 1 and plan.header[10] == 2 and plan.rows_per_tile == 64
 
 
 def _bwd_args(fwd=None, **kw):
@@ -281,10 +348,11 @@ def test_workspace_and_capacity():
     rows, _, per = _lib.tile_shape(4, 2, 64)
     tiles = min(-(-1000 // rows) + 3, 3 * -(-600 // rows))
     slots = 2 * 256 * TILES_PER_CU[(64, False)] // (4 // per)
-    assert entries.value == 8 + 4 * min(tiles, slots // 2) + 4 * (tiles + slots)
+    assert entries.value == _lib.PLAN_HEADER + 4 * min(tiles, slots // 2) + 4 * (tiles + slots)
     assert lib.karpo_attn_workspace_bytes(ctypes.byref(a), ctypes.byref(size)) == 0
     partial = slots * (4 // per) * 128 * (64 + 2) * 4
-    assert size.value >= 4 * (entries.value + 4) + partial and size.value % 256 == 0
+    # the plan, the planner's tile bases (n_seq + 1) and its status word, then the partials
+    assert size.value >= 4 * (entries.value + 4 + 1) + partial and size.value % 256 == 0
 
 
 def test_python_plan_object():
@@ -292,12 +360,13 @@ def test_python_plan_object():
     plan = ops.make_plan([0, 100, 400], [0, 100, 400], 32, 16, 128, -1, 0, device="cpu", max_q=70000)
     # tiles of 2, 3 and 5 key steps, none longer than the shortest split (8 steps)
     assert plan.items == 3 and plan.rows_per_tile == 192 and plan.split_tiles == 0
-    assert plan.tensor.dtype.is_signed and plan.tensor.numel() == 8 + 4 * plan.items
-    assert plan.header == [3, 192, 64, 2, 0, 12, 8, 0]
+    assert plan.tensor.dtype.is_signed and plan.tensor.numel() == _lib.PLAN_HEADER + 4 * plan.items
+    assert plan.header == (3, 192, 64, 2, 0, 12, 12, 0, 2, 0, 3, 0)
+    assert plan.n_seq == 2 and not plan.gather
     # the default max_q (the longest run, 300): small tiles of 64 rows, 32-key steps, 4 waves; tiles of 2, 4 and 2, 4,
     # 6, 8, 10 steps: the 10-step tile is longer than the shortest split and takes two parts
     small = ops.make_plan([0, 100, 400], [0, 100, 400], 32, 16, 128, -1, 0, device="cpu")
-    assert small.header[1:6] == [64, 32, 2, 1, 4] and small.items == 2 + 5 + 1
+    assert small.header[1:6] == (64, 32, 2, 1, 4) and small.items == 2 + 5 + 1
     long = ops.make_plan([0, 3000], [0, 3000], 32, 16, 128, -1, 0, device="cpu", max_q=70000)
     # 16 tiles of 3, 6, .., 45 and 47 steps: 407 x 16 = 6512 workgroup-steps over 256, parts of at most 26 steps
     assert long.split_tiles == 8 and long.items == 16 + 8
@@ -315,10 +384,27 @@ def test_planned_call_refuses_bounds_past_the_tensors():
     cu = torch.zeros(3, dtype=torch.int32)
     with pytest.raises(ValueError, match="900 key rows"):
         ops.run(q, k, k, cu, cu, 300, 0.1, -1, 0, None, plan)
-    with pytest.raises(ValueError, match="row table"):
-        ops.run(q, k, k, cu, cu, 300, 0.1, -1, 0, None, plan, key_rows=torch.zeros(800, dtype=torch.int32))
+    gathered = ops.make_plan([0, 100, 400], [0, 300, 900], 4, 2, 64, -1, 0, device="cpu", gather=True)
+    with pytest.raises(ValueError, match="the row table has 800"):
+        ops.run(q, k, k, cu, cu, 300, 0.1, -1, 0, None, gathered, key_rows=torch.zeros(800, dtype=torch.int32))
     with pytest.raises(ValueError, match="query rows"):
-        ops.run(q[:399], k, k, cu, cu, 300, 0.1, -1, 0, None, plan, key_rows=torch.zeros(900, dtype=torch.int32))
+        ops.run(q[:399], k, k, cu, cu, 300, 0.1, -1, 0, None, gathered,
+                key_rows=torch.zeros(900, dtype=torch.int32))
+
+
+def test_planned_call_refuses_another_pack_or_row_table_use():
+    """A plan is for its own sequence count, row-table use and max_q: calls that differ are refused on the host."""
+    plan = ops.make_plan([0, 100, 400], [0, 300, 900], 4, 2, 64, -1, 0, device="cpu")
+    q = torch.zeros(400, 4, 64, dtype=torch.bfloat16)
+    k = torch.zeros(900, 2, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="2 sequences, the call has 3"):
+        ops.run(q, k, k, torch.zeros(4, dtype=torch.int32), torch.zeros(4, dtype=torch.int32), 300, 0.1, -1, 0, None,
+                plan)
+    cu = torch.zeros(3, dtype=torch.int32)
+    with pytest.raises(ValueError, match="without a row table"):
+        ops.run(q, k, k, cu, cu, 300, 0.1, -1, 0, None, plan, key_rows=torch.zeros(900, dtype=torch.int32))
+    with pytest.raises(ValueError, match="below the plan's 300"):
+        ops.run(q, k, k, cu, cu, 299, 0.1, -1, 0, None, plan)
 
 
 @pytest.mark.parametrize("q_cu,k_cu,left,right,spans", [
@@ -360,3 +446,26 @@ def test_registered_operators_have_fake_kernels():
         assert (lse.shape, lse.dtype) == ((4, 10), torch.float32)
         dq, dk, dv = torch.ops.karpo_amd.packed_attention_backward(o, q, k, k, o, lse, cu, cu, 8, 0.1, -1, 0, None)
         assert (dq.shape, dk.shape, dv.shape) == (q.shape, k.shape, k.shape)
+
+
+def test_norm_rope_refuses_tables_that_do_not_fit():
+    """karpo_attn_norm_rope reads weight[d] and cos / sin rows up to x's rows: tables that do not cover them are
+    refused before any launch (shapes only: fake tensors on the GPU device)."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    with FakeTensorMode():
+        x = torch.empty(10, 2, 128, dtype=torch.bfloat16, device="cuda")
+        bf = dict(dtype=torch.bfloat16, device="cuda")
+        with pytest.raises(ValueError, match="weight"):
+            ops.norm_rope(x, ops.Norm(ops.NORM_WEIGHT, torch.empty(64, **bf), 1e-6))
+        with pytest.raises(ValueError, match="weight"):
+            ops.norm_rope(x, ops.Norm(ops.NORM_ONE_PLUS, None, 1e-6))
+        norm = ops.Norm(ops.NORM_WEIGHT, torch.empty(128, **bf), 1e-6)
+        for cos, sin in ((torch.empty(9, 128, **bf), torch.empty(9, 128, **bf)),  # fewer rows than x
+                         (torch.empty(10, 128, **bf), torch.empty(10, 64, **bf)),  # two shapes
+                         (torch.empty(10, 256, **bf), torch.empty(10, 256, **bf)),  # wider than the head
+                         (torch.empty(10, 2, 128, **bf), torch.empty(10, 2, 128, **bf))):  # not a table
+            with pytest.raises(ValueError, match="rope tables"):
+                ops.norm_rope(x, norm, (cos, sin))
+        with pytest.raises(ValueError, match="out must"):
+            ops.norm_rope(x, norm, out=torch.empty(10, 2, 64, **bf))
