@@ -46,8 +46,9 @@ enum {
   KARPO_ATTN_ERR_CAPACITY = 10,   /* karpo_attn_plan: the output buffer is too small */
   KARPO_ATTN_ERR_BOUNDS = 11,     /* karpo_attn_plan: host bounds not non-decreasing from 0 */
   KARPO_ATTN_ERR_PROLOGUE = 12,   /* a norm mode, weight, rope table or gate the kernel cannot take */
-  KARPO_ATTN_ERR_PLAN = 13        /* a host plan made for another call: its tile geometry, row-table use, sequence
+  KARPO_ATTN_ERR_PLAN = 13,       /* a host plan made for another call: its tile geometry, row-table use, sequence
                                      count or sizes do not match this call's, or its header copy is missing */
+  KARPO_ATTN_ERR_SCRATCH = 14     /* karpo_attn_fwd_noalloc: the call needs more scratch than its 144 MiB */
 };
 
 /* Int32 entries of a plan's header (see karpo_attn_plan). */
@@ -194,6 +195,16 @@ int karpo_attn_plan_capacity(const KarpoAttnArgs* args, int64_t* entries);
  * total_q, every query run at most max_q); device bounds that break it are not planned (nothing is launched past the
  * planner, no row is read or written) and leave KARPO_ATTN_ERR_BOUNDS in the workspace's status word. */
 int karpo_attn_fwd(const KarpoAttnArgs* args, void* stream);
+
+/* karpo_attn_fwd without a workspace: no counterpart in the reference; for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid allocation). args->workspace is ignored:
+ * the scratch (device plan, planner tile bases and status word, partials of split tiles) is a 144 MiB device array of
+ * the library, which a device holds from this entry point's first call on it until the process ends. Calls whose
+ * karpo_attn_workspace_bytes exceeds 144 MiB are refused with KARPO_ATTN_ERR_SCRATCH before anything runs. Every
+ * call on one device shares that device's array (nothing in it needs to start at zero: each call's planner and
+ * kernels write what they read), so calls that overlap on one device race; serialise them (one stream, or events).
+ * Allocates nothing: no hipMalloc, no hipFree. */
+int karpo_attn_fwd_noalloc(const KarpoAttnArgs* args, void* stream);
 
 /* The status word the device planner of the last karpo_attn_fwd call on this workspace (args->plan NULL) left:
  * KARPO_ATTN_OK, or KARPO_ATTN_ERR_BOUNDS when the device bounds broke the contract and nothing was computed.

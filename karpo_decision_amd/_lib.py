@@ -12,16 +12,17 @@ LIBRARY = Path(__file__).resolve().parent / "libkarpo_attn.so"
 #: Every symbol ``include/karpo_attn.h`` declares.
 EXPORTS = ("karpo_attn_fwd", "karpo_attn_plan", "karpo_attn_plan_capacity", "karpo_attn_workspace_bytes",
            "karpo_attn_tile_shape", "karpo_attn_strerror", "karpo_attn_version", "karpo_attn_norm_rope",
-           "karpo_attn_bwd_workspace_bytes", "karpo_attn_bwd", "karpo_attn_device_status")
+           "karpo_attn_bwd_workspace_bytes", "karpo_attn_bwd", "karpo_attn_device_status",
+           "karpo_attn_fwd_noalloc")
 
 OK = 0
 ERR_HEAD_DIM, ERR_HEADS, ERR_LAYOUT, ERR_WINDOW, ERR_SPANS, ERR_ARG, ERR_BOUNDS = 2, 3, 4, 6, 7, 9, 11
-ERR_PROLOGUE, ERR_PLAN = 12, 13
+ERR_PROLOGUE, ERR_PLAN, ERR_SCRATCH = 12, 13, 14
 #: Int32 entries of a plan's header (KARPO_ATTN_PLAN_HEADER).
 PLAN_HEADER = 12
 #: Status codes that mean "these arguments are not supported" (ValueError), the rest are runtime failures.
 VALUE_ERRORS = {1, ERR_HEAD_DIM, ERR_HEADS, ERR_LAYOUT, 5, ERR_WINDOW, ERR_SPANS, ERR_ARG, 10, ERR_BOUNDS,
-                ERR_PROLOGUE, ERR_PLAN}
+                ERR_PROLOGUE, ERR_PLAN, ERR_SCRATCH}
 
 
 class KarpoAttnArgs(ctypes.Structure):
@@ -111,6 +112,8 @@ def load() -> ctypes.CDLL:
         lib.karpo_attn_bwd.restype = ctypes.c_int
         lib.karpo_attn_device_status.argtypes = [P(KarpoAttnArgs), ctypes.c_void_p, P(ctypes.c_int32)]
         lib.karpo_attn_device_status.restype = ctypes.c_int
+        lib.karpo_attn_fwd_noalloc.argtypes = [P(KarpoAttnArgs), ctypes.c_void_p]
+        lib.karpo_attn_fwd_noalloc.restype = ctypes.c_int
         _lib = lib
         return lib
 

@@ -25,7 +25,8 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-munsafe-fp-atomics", f"-I{INCLUDE}", f"-I{CSRC}",
 ]
-SOURCES = ["attn_fwd.hip", "attn_fwd_128.hip", "attn_bwd.hip", "attn_bwd_pair.hip", "capi.cpp", "plan.cpp"]
+SOURCES = ["attn_fwd.hip", "attn_fwd_128.hip", "attn_bwd.hip", "attn_bwd_pair.hip", "capi.cpp", "plan.cpp",
+           "scratch.hip"]
 # per-source flags: the head-size-128 wide / long forward tiles under the iterative-ILP machine scheduler
 SOURCE_FLAGS = {"attn_fwd_128.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"]}
 

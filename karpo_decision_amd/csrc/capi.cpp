@@ -98,6 +98,8 @@ extern "C" const char* karpo_attn_strerror(int status) {
       return "unsupported fused prologue / gate: norm mode 0-3 with a 16-byte aligned weight for modes 1-2, both rope "
              "tables 16-byte aligned with a row stride that is a multiple of 8, rope_dim a multiple of 32 up to "
              "head_dim, gate strides multiples of 4, q_out only with a prologue";
+    case KARPO_ATTN_ERR_SCRATCH:
+      return "the call needs more scratch than karpo_attn_fwd_noalloc's 144 MiB (use karpo_attn_fwd with a workspace)";
     case KARPO_ATTN_ERR_PLAN:
       return "the plan was made for another call (tile geometry, row-table use, sequence count or sizes differ), or "
              "its host header copy is missing";

@@ -469,3 +469,20 @@ def test_norm_rope_refuses_tables_that_do_not_fit():
                 ops.norm_rope(x, norm, (cos, sin))
         with pytest.raises(ValueError, match="out must"):
             ops.norm_rope(x, norm, out=torch.empty(10, 2, 64, **bf))
+
+
+def test_noalloc_entry_point_refuses_calls_beyond_its_scratch():
+    """karpo_attn_fwd_noalloc takes its scratch from a 144 MiB device array: a call whose workspace is larger (a plan
+    of millions of work items) is refused with its status before any HIP call; argument errors keep their codes."""
+    lib = _lib.load()
+    a = _args(n_seq=5_000_000, total_q=500_000_000, max_q=100, heads=32, kv_heads=16, head_dim=128)
+    a.q_stride_tok, a.o_stride_tok = 32 * 128, 32 * 128
+    a.k_stride_tok = a.v_stride_tok = 16 * 128
+    a.q_stride_head = a.k_stride_head = a.v_stride_head = a.o_stride_head = 128
+    need = ctypes.c_size_t()
+    assert lib.karpo_attn_workspace_bytes(ctypes.byref(a), ctypes.byref(need)) == 0
+    assert need.value > 144 << 20
+    assert lib.karpo_attn_fwd_noalloc(ctypes.byref(a), None) == _lib.ERR_SCRATCH
+    assert "144 MiB" in _lib.message(_lib.ERR_SCRATCH)
+    assert lib.karpo_attn_fwd_noalloc(ctypes.byref(_args(head_dim=96)), None) == _lib.ERR_HEAD_DIM
+    assert lib.karpo_attn_fwd_noalloc(None, None) == 1
