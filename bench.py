@@ -58,20 +58,23 @@ def parse() -> argparse.Namespace:
 
 def cpu_baseline(w, repeats: int) -> dict:
     """The oracle (the reference's per-sequence torch SDPA path) on the host cores, on one KV-head group of the pack
-    (its query heads over every sequence), median of ``repeats`` runs after one warm-up, for bf16 and fp32 inputs;
-    the faster is reported. TFLOP/s counts the same unmasked pairs as the GPU figure."""
+    (the query heads of the first four KV heads over every sequence; 8 of 32 heads at the 32k layer, about 10-30 s of
+    CPU work in all), median of ``repeats`` runs after one warm-up, for bf16 and fp32 inputs;
+    the faster is reported. TFLOP/s counts the same unmasked pairs as the GPU figure; the whole layer's CPU time is
+    extrapolated from the sample (heads are independent: the sample's time times heads / group), and labelled so."""
     import torch
 
     from oracle import attention as oracle_attention
 
     torch.set_num_threads(int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)))
-    group = w.heads // w.kv_heads
+    kv = min(4, w.kv_heads)  # the first KV heads and their query heads: seconds of CPU work per run at 32k
+    group = w.heads // w.kv_heads * kv
     from oracle import prologue as oracle_prologue
 
     key, value = w.gathered()
     q = w.query[:, :group].cpu()
-    k = key[:, :1].cpu()
-    v = value[:, :1].cpu()
+    k = key[:, :kv].cpu()
+    v = value[:, :kv].cpu()
     weight = w.q_norm[1].cpu() if w.q_norm is not None else None
     rope = tuple(t.cpu() for t in w.rope) if w.rope is not None else None
     gate = w.gate[:, :group].cpu() if w.gate is not None else None
@@ -106,10 +109,13 @@ def cpu_baseline(w, repeats: int) -> dict:
     except OSError:
         pass
     dtype, sec = best
+    scale = w.heads / group  # the sample is one KV head's query heads: the whole layer's CPU time is this times it
     return {
         "value": round(sample_flops / sec / 1e12, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
-        "kind": "port",
-        "sample": (f"{w.name}: query heads 0-{group - 1} (KV head 0) of {w.heads}, all {w.tokens} tokens; "
+        "kind": "port", "extrapolated": True, "sample_fraction": round(1 / scale, 6),
+        "full_layer_seconds_estimate": round(sec * scale, 3),
+        "sample": (f"{w.name}: query heads 0-{group - 1} (KV heads 0-{kv - 1}) of {w.heads}, "
+                   f"all {w.tokens} tokens; "
                    f"torch {torch.__version__} CPU SDPA per sequence; median of {repeats} after 1 warm-up; "
                    f"seconds bf16 {times_by_dtype['bfloat16']:.3f}, fp32 {times_by_dtype['float32']:.3f}; "
                    f"reported {str(dtype).split('.')[-1]}; os.cpu_count()={os.cpu_count()}; {cpu_model}"),
@@ -180,8 +186,10 @@ def cpu_backward_baseline(w) -> dict:
                                   dtype=torch.float32)
     sec = time.perf_counter() - t0
     sample_flops = 2.5 * w.flops() * group / w.heads
+    scale = w.heads / group
     return {"value": round(sample_flops / sec / 1e12, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
-            "kind": "port",
+            "kind": "port", "extrapolated": True, "sample_fraction": round(1 / scale, 6),
+            "full_layer_seconds_estimate": round(sec * scale, 3),
             "sample": (f"{w.name} backward: query heads 0-{group - 1} (KV head 0) of {w.heads}, all {w.tokens} "
                        f"tokens; torch {torch.__version__} CPU SDPA per sequence + autograd, float32, one run "
                        f"{sec:.3f} s; os.cpu_count()={os.cpu_count()}")}

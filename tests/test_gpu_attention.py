@@ -22,7 +22,7 @@ import pytest
 import torch
 
 import golden_io
-from karpo_decision_amd import _lib, global_attention, hip_attention, ops, sliding_attention, varlen, workloads
+from karpo_decision_amd import _lib, global_attention, hip_attention, ops, sliding_attention, varlen, vision, workloads
 from oracle import attention as oa
 
 pytestmark = pytest.mark.gpu
@@ -889,3 +889,36 @@ def test_device_planner_refuses_bounds_that_break_the_contract(gpu):
     status = []
     _c_abi_call(q, k, k, o, cu_t, cu_t, 200, 0.125, -1, 0, status=status)
     assert status == [_lib.OK] and not torch.isnan(o).any()
+
+
+def test_branched_sliding_pack_with_row_tables_and_image_spans(gpu):
+    """A sliding layer of a block plan with images in the shared blocks and in branches (the reference's image
+    layouts), its branch keys read through the plan's s_rows table and the images' spans folded into the same
+    launch: against the oracle on the gathered keys with the spans (the spans' semantics against rule_a | same-image
+    are pinned on the CPU, tests/test_vision.py)."""
+    from test_vision import LAYOUTS, SOFT, WINDOW, pack, sliding_plan
+
+    seqs = (LAYOUTS["images-in-the-shared-block-and-two-branches"]() + LAYOUTS["image-in-a-branch"]()
+            + LAYOUTS["branch-image-within-a-window-of-the-shared-block"]())
+    ids, seg, _, bounds, spans = pack(seqs)
+    found = vision.soft_token_spans(ids, SOFT, WINDOW, bounds)
+    assert found == spans
+    q_cu, s_cu, s_rows = sliding_plan(seg, bounds, WINDOW)
+    heads, kv_heads, head = 16, 8, 256
+    torch.manual_seed(33)
+    total = len(ids)
+    q = torch.randn(total, heads, head, device=gpu).bfloat16()
+    k = torch.randn(total, kv_heads, head, device=gpu).bfloat16()
+    v = torch.randn(total, kv_heads, head, device=gpu).bfloat16()
+    qc, sc = (torch.tensor(x, dtype=torch.int32, device=gpu) for x in (q_cu, s_cu))
+    sr = torch.tensor(s_rows, dtype=torch.int32, device=gpu)
+    span_t = vision.span_tensor(found, gpu)
+    max_q = max(b - a for a, b in zip(q_cu[:-1], q_cu[1:]))
+    max_s = max(b - a for a, b in zip(s_cu[:-1], s_cu[1:]))
+    for scale in (head ** -0.5, 1.0):
+        with torch.inference_mode():
+            got = sliding_attention.attend(q, k, v, qc, sc, max_q, max_s, scale, WINDOW - 1, spans=span_t, rows=sr)
+        gathered = torch.tensor(s_rows)
+        want = oa.packed_attention(q.cpu(), k.cpu()[gathered], v.cpu()[gathered], q_cu, s_cu, scale, WINDOW - 1, 0,
+                                   found)
+        assert_close(got, want, f"branched sliding pack with spans and s_rows, scale {scale}")
