@@ -4,6 +4,7 @@ missing this module raises, it never falls back to another implementation."""
 from __future__ import annotations
 
 import ctypes
+import functools
 import threading
 from pathlib import Path
 
@@ -150,10 +151,12 @@ def kernel_shape(heads: int, kv_heads: int, head_dim: int, max_q: int = LONG, ga
     return 0
 
 
+@functools.lru_cache(maxsize=1024)
 def tile_shape(heads: int, kv_heads: int, head_dim: int, max_q: int = LONG,
                gather: bool = False) -> tuple[int, int, int]:
     """(query rows per tile, keys per step, query heads per work item) for packs whose longest query run is
-    ``max_q`` (one-wave tiles when every run fits one), read through a row table when ``gather``."""
+    ``max_q`` (one-wave tiles when every run fits one), read through a row table when ``gather`` (memoised: a pure
+    function of its arguments, asked on every planned call)."""
     rows, keys, per = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
     check(load().karpo_attn_tile_shape(heads, kv_heads, head_dim, max_q, int(bool(gather)), ctypes.byref(rows),
                                        ctypes.byref(keys), ctypes.byref(per)), "karpo_attn_tile_shape")

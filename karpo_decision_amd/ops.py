@@ -64,6 +64,31 @@ def _is_gfx950(device: torch.device) -> bool:
     return getattr(props, "gcnArchName", "").split(":")[0] == "gfx950"
 
 
+# The current stream's handle: torch's raw-stream accessor (what its compiled kernels call on every launch), a few
+# microseconds cheaper per call than building a Stream object.
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _current_stream(index: int) -> int:
+    return _raw_stream(index) if _raw_stream is not None else torch.cuda.current_stream(index).cuda_stream
+
+
+class _Noop:
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        return False
+
+
+_NOOP = _Noop()
+
+
+def _on_device(index: int):
+    """torch.cuda.device(index) only when another device is current (entering it costs microseconds per call)."""
+    return _NOOP if torch.cuda.current_device() == index else torch.cuda.device(index)
+
+
 def check_inputs(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_cu: Tensor) -> None:
     """ValueError for anything the kernel does not take (before any launch)."""
     if query.dim() != 3 or key.dim() != 3 or value.dim() != 3:
@@ -80,9 +105,10 @@ def check_inputs(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_cu: 
     for name, t in (("query", query), ("key", key), ("value", value)):
         if t.dtype != torch.bfloat16:
             raise ValueError(f"{name} must be bfloat16, not {t.dtype} (the kernel computes bf16 MFMA products)")
-        if t.stride(2) != 1 or t.stride(0) % 8 or t.stride(1) % 8:
+        st = t.stride()
+        if st[2] != 1 or st[0] % 8 or st[1] % 8:
             raise ValueError(f"{name} needs a contiguous head_dim and row/head strides that are multiples of 8 "
-                             f"(strides {t.stride()})")
+                             f"(strides {st})")
     for name, t in (("q_cu", q_cu), ("k_cu", k_cu)):
         if t.dtype != torch.int32 or t.dim() != 1:
             raise ValueError(f"{name} must be a 1-D int32 tensor, got {t.dtype} {tuple(t.shape)}")
@@ -190,7 +216,8 @@ def _attention_impl(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_c
     if query.shape[0] == 0:
         return out
     q_cu, k_cu = q_cu.contiguous(), k_cu.contiguous()
-    with torch.cuda.device(query.device):
+    index = query.device.index
+    with _on_device(index):
         args = _args(query, key, value, out, q_cu, k_cu, q_cu.numel() - 1, max_q, scale, window_left, window_right,
                      spans, plan, plan_header, key_rows, q_norm, q_norm_eps, q_norm_weight, rope_cos, rope_sin,
                      gate)
@@ -204,8 +231,8 @@ def _attention_impl(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_c
             # the device plan and the fp32 partials of split tiles, from the caching allocator (stream-ordered reuse)
             workspace = torch.empty(need.value, dtype=torch.uint8, device=query.device)
             args.workspace, args.workspace_bytes = workspace.data_ptr(), need.value
-        stream = torch.cuda.current_stream(query.device).cuda_stream
-        _lib.check(lib.karpo_attn_fwd(ctypes.byref(args), ctypes.c_void_p(stream)), "packed attention")
+        _lib.check(lib.karpo_attn_fwd(ctypes.byref(args), ctypes.c_void_p(_current_stream(index))),
+                   "packed attention")
     return out
 
 
@@ -386,8 +413,8 @@ def norm_rope(x: Tensor, norm: Norm | None, rope: tuple[Tensor, Tensor] | None =
         cos, sin = (_bf16_table(t, x.device) for t in rope)
         keep += [cos, sin]
         a.rope_cos, a.rope_sin, a.rope_stride, a.rope_dim = cos.data_ptr(), sin.data_ptr(), cos.stride(0), cos.shape[-1]
-    with torch.cuda.device(x.device):
-        stream = torch.cuda.current_stream(x.device).cuda_stream
+    with _on_device(x.device.index):
+        stream = _current_stream(x.device.index)
         _lib.check(lib.karpo_attn_norm_rope(ctypes.byref(a), ctypes.c_void_p(stream)), "norm_rope")
     # converted tables in `keep` go back to the stream-ordered caching allocator after the launch: safe to reuse
     return out
@@ -418,13 +445,13 @@ def packed_attention_lse(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor
     if query.shape[0] == 0:
         return out, lse
     q_cu, k_cu = q_cu.contiguous(), k_cu.contiguous()
-    with torch.cuda.device(query.device):
+    with _on_device(query.device.index):
         args = _args(query, key, value, out, q_cu, k_cu, q_cu.numel() - 1, max_q, scale, window_left, window_right,
                      spans, None)
         args.lse = lse.data_ptr()
         workspace = _workspace(lib, lib.karpo_attn_workspace_bytes, args, query.device)
         args.workspace, args.workspace_bytes = workspace.data_ptr(), workspace.numel()
-        stream = torch.cuda.current_stream(query.device).cuda_stream
+        stream = _current_stream(query.device.index)
         _lib.check(lib.karpo_attn_fwd(ctypes.byref(args), ctypes.c_void_p(stream)), "packed attention")
     return out, lse
 
@@ -455,7 +482,7 @@ def packed_attention_backward(grad: Tensor, query: Tensor, key: Tensor, value: T
     if query.shape[0] == 0:
         return dq, dk.zero_(), dv.zero_()
     q_cu, k_cu = q_cu.contiguous(), k_cu.contiguous()
-    with torch.cuda.device(query.device):
+    with _on_device(query.device.index):
         b = _lib.KarpoAttnBwdArgs()
         b.fwd = _args(query, key, value, out, q_cu, k_cu, q_cu.numel() - 1, max_q, scale, window_left, window_right,
                       spans, None)
@@ -467,7 +494,7 @@ def packed_attention_backward(grad: Tensor, query: Tensor, key: Tensor, value: T
         b.d_v, b.d_v_stride_tok, b.d_v_stride_head = dv.data_ptr(), dv.stride(0), dv.stride(1)
         workspace = _workspace(lib, lib.karpo_attn_bwd_workspace_bytes, b, query.device)
         b.fwd.workspace, b.fwd.workspace_bytes = workspace.data_ptr(), workspace.numel()
-        stream = torch.cuda.current_stream(query.device).cuda_stream
+        stream = _current_stream(query.device.index)
         _lib.check(lib.karpo_attn_bwd(ctypes.byref(b), ctypes.c_void_p(stream)), "packed attention backward")
     return dq, dk, dv
 
