@@ -454,7 +454,10 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
   f32x16 acc[OB];
 #pragma unroll
   for (int db = 0; db < OB; ++db) acc[db] = f32x16{};
-  float m = -INFINITY, l = 0.f;
+  // the running maximum starts finite: before the first visible key exp2(logit - m) is exp2(-inf) = 0 all the same,
+  // and a rescale from it multiplies zeros (a part that sees no key stores m = -1e30 and l = 0: the merge gives it
+  // weight 1 over zero sums, so an empty row still comes out 0 with LSE -inf)
+  float m = -1e30f, l = 0.f;
   const float c = p.c;
   const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
 
@@ -584,22 +587,19 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
 #pragma unroll
         for (int db = 0; db < OB; ++db) acc[db] *= alpha;
       }
-      const float msub = m == -INFINITY ? 0.f : m;
       bf16x8 pb[KC];
-      float part[2] = {0.f, 0.f};
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc) {
 #pragma unroll
         for (int t = 0; t < 8; t += 2) {
-          const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[kc >> 1][(kc & 1) * 8 + t], c, -msub));
-          const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[kc >> 1][(kc & 1) * 8 + t + 1], c, -msub));
+          const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[kc >> 1][(kc & 1) * 8 + t], c, -m));
+          const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[kc >> 1][(kc & 1) * 8 + t + 1], c, -m));
           const bf16x2 pr = {(__bf16)e0, (__bf16)e1};
           pb[kc][t] = pr[0];
           pb[kc][t + 1] = pr[1];
-          part[(t >> 1) & 1] = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, part[(t >> 1) & 1], false);
+          l = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, l, false);  // l sums the bf16 P the product uses
         }
       }
-      l += part[0] + part[1];
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc) {
 #pragma unroll

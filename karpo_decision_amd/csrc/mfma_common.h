@@ -38,9 +38,11 @@ __device__ __forceinline__ int v_offset(int k, int d) {
   return ((k >> 2) * (D / 16) + (d >> 4)) * 128 + (k & 3) * 32 + (d & 15) * 2;
 }
 
+// The maximum over a lane and the lane 32 away. IEEE maximum (NaN-propagating): one v_maximum3_f32, where fmaxf would
+// first quiet both swapped values.
 __device__ __forceinline__ float half_swap_max(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return __builtin_elementwise_maximum(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 __device__ __forceinline__ float half_swap_sum(float x) {
