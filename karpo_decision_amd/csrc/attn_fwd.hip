@@ -581,7 +581,7 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
       const bool need = mt > m + p.tau;
       if (__builtin_amdgcn_ballot_w64(need)) {  // raise the running maximum (rare after the first steps)
         const float mn = need ? mt : m;
-        const float alpha = need ? __builtin_amdgcn_exp2f(m - mn) : 1.f;  // m = -inf, mt finite: alpha = 0
+        const float alpha = need ? __builtin_amdgcn_exp2f(m - mn) : 1.f;  // from the start value: alpha = 0
         m = mn;
         l *= alpha;
 #pragma unroll
