@@ -676,6 +676,343 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
   }
 }
 
+#if KA_FWD_UNIT == 0
+// ---- the head-size-512 wide tile as a ping-pong (calls without a row table)
+//
+// attn_fwd_kernel's pair tile runs its eight waves in lockstep: every SIMD does its two waves' QK^T halves together,
+// then both softmaxes, then both P.V halves, two barriers per step. Here the four pairs form two groups that
+// alternate, phase by phase, between an MFMA phase (this wave's half of QK^T of step s and of P.V of step s - 1, then
+// its partial scores to its exchange slot) and a VALU phase (the partner's partial added, the step's softmax), so one
+// group's MFMAs run beside the other's softmax. Pairs 0, 1 (waves 0-3) form group A, pairs 2, 3 group B: the waves of
+// a workgroup are dealt to the SIMDs in turn, so waves w and w + 4 share one, one of each group (a different deal
+// would cost speed, not correctness: every wave meets the same barriers, and a pair is always in one group). T(s)
+// holds K(s) and V(s - 1) (both are read in iteration s); it is copied during iteration s - 1 into the buffer T(s - 2)
+// left and waited for at that iteration's end. The phase barriers are bare s_barrier instructions (each wave waits for
+// its own LDS work and copies explicitly), so the copies stay in flight across the middle barrier. The arithmetic is
+// attn_fwd_kernel's but for the order in which l adds up a step's 16 P values (two partial sums).
+
+// s_barrier without the fence __syncthreads adds (which waits for every outstanding copy)
+__device__ __forceinline__ void bare_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+__global__ __launch_bounds__(512, 2) void attn_fwd_pair_pp_kernel(Params p) {
+  constexpr int D = 512, W = 8, BN = 32;
+  constexpr int DC = D / 16, DB = D / 32;
+  constexpr int QC = DC / 2, OB = DB / 2;  // this wave's half of D
+  constexpr int KC = BN / 16;
+  constexpr int TILE = BN * D * 2;        // 32 KiB
+  constexpr int BLKS = TILE / 1024;       // 32
+  constexpr int INSTS = BLKS / W;         // 4 per wave and tile
+  static_assert(BLKS % W == 0, "every wave copies the same number of blocks");
+  __shared__ __attribute__((aligned(1024))) char k_lds0[TILE];
+  __shared__ __attribute__((aligned(1024))) char k_lds1[TILE];
+  __shared__ __attribute__((aligned(1024))) char v_lds0[TILE];
+  __shared__ __attribute__((aligned(1024))) char v_lds1[TILE];
+  __shared__ __attribute__((aligned(16))) f32x4 xch[W][4 * 64];  // a wave's 16 partial scores per lane
+  int(*red)[W] = (int(*)[W])&xch[0][0];                           // the envelope (read before the first exchange)
+  auto kbuf = [&](int i) -> KA_LDS char* { return i == 0 ? (KA_LDS char*)k_lds0 : (KA_LDS char*)k_lds1; };
+  auto vbuf = [&](int i) -> KA_LDS char* { return i == 0 ? (KA_LDS char*)v_lds0 : (KA_LDS char*)v_lds1; };
+
+  if (p.plan[2] != BN || p.plan[5] != W) return;
+  const int n_items = p.plan[0];
+  const int item = blockIdx.x / p.n_hg;
+  const int hg = blockIdx.x - item * p.n_hg;
+  if (item >= n_items) return;
+  const int32_t* entry = p.plan + p.plan[6] + kItemInts * item;
+  const int seg = entry[0];
+  const int tile = entry[1];
+  const int part = entry[2] & 0xffff, parts = entry[2] >> 16;
+  const int slot = entry[3];
+  if (parts > 1 && (slot < 0 || slot + part >= p.slots)) return;
+  const int rows_per_tile = p.plan[1];
+  const int qa = p.q_cu[seg], lq = p.q_cu[seg + 1] - qa;
+  const int ka = p.k_cu[seg], lk = p.k_cu[seg + 1] - ka;
+  const int kvh = (hg * p.ng) / p.group;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 31, half = lane >> 5;
+  const int dh = wave & 1;
+  const int grp = wave >> 2;
+  const int vec = (wave >> 1) * 32 + col;
+  const int off = vec / p.ng;
+  const int pos = tile * rows_per_tile + off;
+  const int head = hg * p.ng + (vec - off * p.ng);
+  const bool valid = pos < lq;
+  int lo = 0, hi = 0, sl = 0, sh = 0;
+  int wlo = INT32_MAX, whi = INT32_MIN, wflo = INT32_MIN, wfhi = INT32_MAX;
+  if (valid) {
+    const LaneKeys lk_ = lane_keys(pos, qa, lq, lk, p.left, p.right, p.spans, p.n_spans);
+    lo = lk_.lo;
+    hi = lk_.hi;
+    sl = lk_.sl;
+    sh = lk_.sh;
+    wflo = lo;
+    wfhi = hi;
+    if (lo < hi) {
+      wlo = lo;
+      whi = hi;
+    }
+    if (sl < sh) {
+      wlo = min(wlo, sl);
+      whi = max(whi, sh);
+    }
+  }
+  wlo = __builtin_amdgcn_readfirstlane(wave_min(wlo));
+  whi = __builtin_amdgcn_readfirstlane(wave_max(whi));
+  wflo = __builtin_amdgcn_readfirstlane(wave_max(wflo));
+  wfhi = __builtin_amdgcn_readfirstlane(wave_min(wfhi));
+  if (lane == 0) {
+    red[0][wave] = wlo;
+    red[1][wave] = whi;
+  }
+
+  bf16x8 qop[QC];
+  {
+    const uint16_t* qrow = p.q + (int64_t)(qa + pos) * p.sq_t + (int64_t)head * p.sq_h;
+    u32x4 x[QC];
+#pragma unroll
+    for (int i = 0; i < QC; ++i) {
+      x[i] = u32x4{0, 0, 0, 0};
+      if (valid) x[i] = *(const u32x4*)(qrow + half * 8 + (dh * QC + i) * 16);
+    }
+    if (p.q_norm != KARPO_NORM_NONE || p.rope_cos != nullptr) {
+      if (valid) query_prologue<D, QC>(p, qrow, (int64_t)(qa + pos), half, dh * QC, x);
+      if (p.q_out != nullptr && valid && part == 0) {
+        uint16_t* qo = p.q_out + (int64_t)(qa + pos) * p.sqo_t + (int64_t)head * p.sqo_h + half * 8;
+#pragma unroll
+        for (int i = 0; i < QC; ++i) *(u32x4*)(qo + (dh * QC + i) * 16) = x[i];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < QC; ++i) qop[i] = __builtin_bit_cast(bf16x8, x[i] ^ p.qsign);
+  }
+  __syncthreads();
+  int klo = wlo, khi = whi;
+#pragma unroll
+  for (int w = 0; w < W; ++w) {
+    klo = min(klo, red[0][w]);
+    khi = max(khi, red[1][w]);
+  }
+  klo = __builtin_amdgcn_readfirstlane(klo);
+  khi = __builtin_amdgcn_readfirstlane(khi);
+  int j_first, n_steps;
+  part_steps(klo, khi, BN, part, parts, &j_first, &n_steps);
+
+  const uint16_t* kbase = p.k + (int64_t)kvh * p.sk_h + (int64_t)ka * p.sk_t;
+  const uint16_t* vbase = p.v + (int64_t)kvh * p.sv_h + (int64_t)ka * p.sv_t;
+  // a wave's INSTS copy blocks of a tile share their rows: block r starts r * 64 bytes (K) / r * 256 bytes (V) after
+  // block 0 in memory, so one offset register per tile kind
+  uint32_t k_voff0, v_voff0;
+  {
+    int key, colm;
+    k_dma_source<D>(wave * INSTS, lane, &key, &colm);
+    k_voff0 = (uint32_t)(key * p.sk_t + colm) * 2u;
+    v_dma_source<D>(wave * INSTS, lane, &key, &colm);
+    v_voff0 = (uint32_t)(key * p.sv_t + colm) * 2u;
+  }
+  // T(t) = K(t), V(t - 1): running pointers, empty ranges past the ends (every wave issues 2 INSTS copies per T)
+  const uint16_t* ck = kbase + (int64_t)j_first * p.sk_t;
+  const uint16_t* cv = vbase + (int64_t)j_first * p.sv_t;
+  const int64_t k_step = (int64_t)BN * p.sk_t, v_step = (int64_t)BN * p.sv_t;
+  const int j_end = j_first + n_steps * BN;
+  int jt = j_first;
+  auto copy_T = [&](int b) {
+    const int rk = jt < j_end ? min(lk - jt, BN) : 0;
+    const int rv = jt > j_first && jt <= j_end ? min(lk - (jt - BN), BN) : 0;
+#pragma unroll
+    for (int r = 0; r < INSTS; ++r) {
+      dma_16b(ck, rk * (int)p.sk_t * 2, kbuf(b) + (wave * INSTS + r) * 1024, k_voff0 + 64u * r);
+      dma_16b(cv, rv * (int)p.sv_t * 2, vbuf(b) + (wave * INSTS + r) * 1024, v_voff0 + 256u * r);
+    }
+    if (jt < j_end) ck += k_step;
+    if (jt > j_first && jt <= j_end) cv += v_step;
+    jt += BN;
+  };
+
+  const int k_read = k_offset<D>(key_row(col), half) + dh * QC * 512;
+  const int g = lane >> 4, jl = lane & 15;
+  const int v_read = v_offset<D>(8 * (g >> 1) + (jl >> 2), 16 * (g & 1) + 4 * (jl & 3)) + dh * OB * 256;
+
+  f32x16 acc[OB];
+#pragma unroll
+  for (int db = 0; db < OB; ++db) acc[db] = f32x16{};
+  float m = -1e30f, l = 0.f;  // finite start, as attn_fwd_kernel
+  const float c = p.c;
+  const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+  f32x16 st;
+  bf16x8 pb[KC];
+  KA_LDS f32x4* my_slot = (KA_LDS f32x4*)&xch[wave][0] + lane;
+  const KA_LDS f32x4* other_slot = (const KA_LDS f32x4*)&xch[wave ^ 1][0] + lane;
+
+  auto active = [&](int t) {
+    const int j0 = j_first + t * BN;
+    return t >= 0 && t < n_steps && j0 < whi && j0 + BN > wlo;
+  };
+  // this wave's half of QK^T(s) and of P.V(s - 1), both on T(s) (buffer b); the partial scores go to the slot
+  auto mfma_phase = [&](int s, int b) {
+    const bool a0 = active(s), a1 = active(s - 1);
+    const KA_LDS char* kt = kbuf(b);
+    const KA_LDS char* vt = vbuf(b);
+    if (a0) {
+      st = f32x16{};
+#pragma unroll
+      for (int dc = 0; dc < QC; ++dc) {
+        const bf16x8 a = *(const KA_LDS bf16x8*)(kt + k_read + dc * 512);
+        st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qop[dc], st, 0, 0, 0);
+      }
+    }
+    if (a1) {
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) {
+#pragma unroll
+        for (int db = 0; db < OB; ++db) {
+          bf16x4 v2[2];
+#pragma unroll
+          for (int rr = 0; rr < 2; ++rr)
+            v2[rr] = __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                                    (KA_LDS s16x4*)(vt + v_read + (kc * 4 + rr) * (D / 16) * 128 + db * 256)));
+          const bf16x8 a = __builtin_shufflevector(v2[0], v2[1], 0, 1, 2, 3, 4, 5, 6, 7);
+          acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[kc], acc[db], 0, 0, 0);
+        }
+      }
+    }
+    if (a0) {
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) my_slot[q4 * 64] = f32x4{st[4 * q4], st[4 * q4 + 1], st[4 * q4 + 2], st[4 * q4 + 3]};
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the slot written, this phase's LDS reads done
+  };
+  // the full scores of step t (this wave's partial plus the partner's, equal in both waves: addition commutes),
+  // then the softmax: both waves of a pair compute the same m, l and P
+  auto valu_phase = [&](int t) {
+    if (!active(t)) return;
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const f32x4 o = other_slot[q4 * 64];
+      st[4 * q4] += o.x;
+      st[4 * q4 + 1] += o.y;
+      st[4 * q4 + 2] += o.z;
+      st[4 * q4 + 3] += o.w;
+    }
+    const int j0 = j_first + t * BN;
+    if (!(j0 >= wflo && j0 + BN <= wfhi)) {
+#pragma unroll
+      for (int jj = 0; jj < 16; ++jj) {
+        const int key = j0 + (jj >> 3) * 16 + half * 8 + (jj & 7);
+        const bool vis = ((unsigned)(key - lo) < (unsigned)(hi - lo)) | ((unsigned)(key - sl) < (unsigned)(sh - sl));
+        st[jj] = vis ? st[jj] : -INFINITY;
+      }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int jj = 0; jj < 16; ++jj) mx = fmaxf(mx, st[jj]);
+    const float mt = half_swap_max(mx) * c;
+    const bool need = mt > m + p.tau;
+    if (__builtin_amdgcn_ballot_w64(need)) {
+      const float mn = need ? mt : m;
+      const float alpha = need ? __builtin_amdgcn_exp2f(m - mn) : 1.f;
+      m = mn;
+      l *= alpha;
+#pragma unroll
+      for (int db = 0; db < OB; ++db) acc[db] *= alpha;
+    }
+    // l in two partial sums (one chain through l kept an array of this kernel in scratch memory)
+    float psum[2] = {0.f, 0.f};
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+#pragma unroll
+      for (int t2 = 0; t2 < 8; t2 += 2) {
+        const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[kc * 8 + t2], c, -m));
+        const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[kc * 8 + t2 + 1], c, -m));
+        const bf16x2 pr = {(__bf16)e0, (__bf16)e1};
+        pb[kc][t2] = pr[0];
+        pb[kc][t2 + 1] = pr[1];
+        psum[(t2 >> 1) & 1] = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, psum[(t2 >> 1) & 1], false);
+      }
+    }
+    l += psum[0] + psum[1];
+  };
+
+  // prologue: T(0) (K(0) only) landed; the envelope slots are read by every wave before the first exchange write
+  if (n_steps > 0) copy_T(0);
+  wait_vmcnt<0>();
+  __syncthreads();
+  if (n_steps > 0) {
+    // iteration s on buffer b = s % 2: T(s + 1) into the other buffer (which held T(s - 1)), waited at the end
+    auto iter_a = [&](int s, int b) {
+      if (s + 1 <= n_steps) copy_T(b ^ 1);
+      mfma_phase(s, b);
+      bare_barrier();
+      valu_phase(s);
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      wait_vmcnt<0>();
+      bare_barrier();
+    };
+    auto iter_b = [&](int s, int b) {
+      if (s + 1 <= n_steps) copy_T(b ^ 1);
+      valu_phase(s - 1);
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      bare_barrier();
+      mfma_phase(s, b);
+      wait_vmcnt<0>();
+      bare_barrier();
+    };
+    if (grp == 0) {
+      int s = 0;
+      for (; s + 1 <= n_steps; s += 2) {
+        iter_a(s, 0);
+        iter_a(s + 1, 1);
+      }
+      if (s <= n_steps) iter_a(s, 0);
+    } else {
+      int s = 0;
+      for (; s + 1 <= n_steps; s += 2) {
+        iter_b(s, 0);
+        iter_b(s + 1, 1);
+      }
+      if (s <= n_steps) iter_b(s, 0);
+    }
+  }
+
+  const float lt = half_swap_sum(l);
+  if (parts > 1) {
+    constexpr int V = 32 * W / 2;
+    float* base = p.partial + partial_base(slot, part, p.n_hg, hg, V, D);
+    float* op = base + (int64_t)vec * D + dh * (D / 2) + half * 4;
+#pragma unroll
+    for (int db = 0; db < OB; ++db)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        float4 x = {acc[db][g4 * 4], acc[db][g4 * 4 + 1], acc[db][g4 * 4 + 2], acc[db][g4 * 4 + 3]};
+        *(float4*)(op + db * 32 + g4 * 8) = x;
+      }
+    if (half == 0 && dh == 0) {
+      base[V * D + vec] = m;
+      base[V * D + V + vec] = lt;
+    }
+    return;
+  }
+  const float inv = lt > 0.f ? 1.f / lt : 0.f;
+  if (valid && p.lse != nullptr && half == 0 && dh == 0)
+    p.lse[(int64_t)head * p.lse_stride + qa + pos] = lt > 0.f ? (m + __log2f(lt)) * 0.69314718055994531f : -INFINITY;
+  if (valid) {
+    uint16_t* op = p.o + (int64_t)(qa + pos) * p.so_t + (int64_t)head * p.so_h + dh * (D / 2) + half * 4;
+    const uint16_t* gp = p.gate != nullptr
+                             ? p.gate + (int64_t)(qa + pos) * p.sg_t + (int64_t)head * p.sg_h + dh * (D / 2) + half * 4
+                             : nullptr;
+#pragma unroll
+    for (int db = 0; db < OB; ++db) {
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        *(u32x2*)(op + db * 32 + g4 * 8) =
+            output4(acc[db][g4 * 4] * inv, acc[db][g4 * 4 + 1] * inv, acc[db][g4 * 4 + 2] * inv,
+                    acc[db][g4 * 4 + 3] * inv, gp != nullptr ? gp + db * 32 + g4 * 8 : nullptr);
+      }
+    }
+  }
+}
+#endif  // KA_FWD_UNIT == 0
+
 // ---- merge: the parts of split tiles. Thread per (split tile, head group, query vector, 4 head-dim elements), in a
 // grid-stride loop over a fixed grid, so every load of a thread is independent and the launch costs little when the
 // plan splits nothing. The parts' running maxima go on a common M: O = sum_p 2^(m_p - M) O_p / sum_p 2^(m_p - M) l_p
@@ -1023,9 +1360,15 @@ static hipError_t launch_attn(const Params& p, int64_t items, int64_t merges, in
                          stream, p);
     else
       return hipErrorInvalidValue;
-  } else
-    hipLaunchKernelGGL((attn_fwd_kernel<D, SHAPE, false>), dim3((unsigned)(items * n_hg)), dim3(64 * Cfg::W), 0,
-                       stream, p);
+  } else {
+#if KA_FWD_UNIT == 0
+    if constexpr (D == 512 && SHAPE == kWide)
+      hipLaunchKernelGGL(attn_fwd_pair_pp_kernel, dim3((unsigned)(items * n_hg)), dim3(64 * Cfg::W), 0, stream, p);
+    else
+#endif
+      hipLaunchKernelGGL((attn_fwd_kernel<D, SHAPE, false>), dim3((unsigned)(items * n_hg)), dim3(64 * Cfg::W), 0,
+                         stream, p);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || merges <= 0) return e;
   constexpr int64_t per_merge = (int64_t)tile_vectors(D, SHAPE) * (D / 4);  // threads of one head group
