@@ -8,7 +8,10 @@
 // plan that leaves a row of a sequence unwritten, or writes one twice, is reported.
 //
 // Test infrastructure only (built by tests/test_replay.py with the host compiler); it mirrors the kernel's control
-// flow (which steps copy, which fetch table rows) by hand, and shares every address formula with it.
+// flow (which steps copy, which fetch table rows) by hand, and shares every address formula with it. At head size 512
+// without a row table the library launches attn_fwd_pair_pp_kernel instead: the same plan items, tiles, bounds and
+// copy sources, its copies of a step's tiles issued one iteration earlier; karpo_replay_pair_blocks checks the one
+// address it forms differently (a block's source as block 0's plus a fixed step).
 #include <stdint.h>
 #include <stdio.h>
 #include <string.h>
@@ -321,5 +324,27 @@ int64_t karpo_replay_fwd(const KarpoAttnArgs* a, const int32_t* q_cu, const int3
     first[first_len - 1] = 0;
   }
   return r.violations;
+}
+
+// The head-size-512 pair ping-pong (attn_fwd_pair_pp_kernel) addresses a wave's `insts` copy blocks of a K (V) tile
+// from block wave * insts plus k_block (v_block) bytes per block: returns how many (wave, lane, block) sources, for
+// these row strides (elements), differ from k_dma_source / v_dma_source of the block itself.
+int64_t karpo_replay_pair_blocks(int waves, int insts, int64_t k_stride, int64_t v_stride, int64_t k_block,
+                                 int64_t v_block) {
+  int64_t bad = 0;
+  for (int w = 0; w < waves; ++w)
+    for (int lane = 0; lane < 64; ++lane) {
+      int k0, c0, v0, d0;
+      k_dma_source<512>(w * insts, lane, &k0, &c0);
+      v_dma_source<512>(w * insts, lane, &v0, &d0);
+      for (int r = 0; r < insts; ++r) {
+        int k, c, v, d;
+        k_dma_source<512>(w * insts + r, lane, &k, &c);
+        v_dma_source<512>(w * insts + r, lane, &v, &d);
+        bad += (k * k_stride + c) * 2 != (k0 * k_stride + c0) * 2 + k_block * r;
+        bad += (v * v_stride + d) * 2 != (v0 * v_stride + d0) * 2 + v_block * r;
+      }
+    }
+  return bad;
 }
 }

@@ -36,6 +36,8 @@ def replay(tmp_path_factory):
                                      ctypes.c_int64, P(ctypes.c_int32), P(ctypes.c_int32), ctypes.c_int64,
                                      ctypes.c_int, P(ctypes.c_int64), ctypes.c_char_p, ctypes.c_int]
     lib.karpo_replay_fwd.restype = ctypes.c_int64
+    lib.karpo_replay_pair_blocks.argtypes = [ctypes.c_int, ctypes.c_int] + [ctypes.c_int64] * 4
+    lib.karpo_replay_pair_blocks.restype = ctypes.c_int64
     return lib
 
 
@@ -154,3 +156,13 @@ def test_the_replay_finds_planted_mistakes(replay):
     # keys past the tensor's rows: the copies read outside the K allocation
     bad, _, first = run_replay(replay, [0, 200], [0, 200], 8, 2, 64, -1, 0, total_k=150)
     assert bad > 0 and "chunk" in first
+
+
+@pytest.mark.parametrize("k_stride,v_stride", [(512, 512), (2048, 2048), (4104, 1032)])
+def test_pair_ping_pong_copy_blocks(replay, k_stride, v_stride):
+    """The head-size-512 ping-pong kernel copies a wave's four blocks of a K (V) tile from one offset register plus 64
+    (256) bytes per block: the same sources as k_dma_source / v_dma_source per block, whatever the row strides (head
+    strides of GQA layouts, padded rows); a wrong per-block step is reported."""
+    assert replay.karpo_replay_pair_blocks(8, 4, k_stride, v_stride, 64, 256) == 0
+    assert replay.karpo_replay_pair_blocks(8, 4, k_stride, v_stride, 32, 256) > 0
+    assert replay.karpo_replay_pair_blocks(8, 4, k_stride, v_stride, 64, 128) > 0
