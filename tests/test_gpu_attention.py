@@ -363,15 +363,19 @@ def test_random_packs_under_every_shape(gpu, seed):
 
 
 def _c_abi_call(q, k, v, o, q_cu, k_cu, max_q, scale, left, right, plan: ops.Plan | None = None, spans=None,
-                status: list | None = None):
-    """One karpo_attn_fwd through the C ABI into ``o``; returns the workspace. With ``status`` (a list) the device
-    planner's status word is appended to it (karpo_attn_device_status)."""
+                status: list | None = None, gate=None, lse=None):
+    """One karpo_attn_fwd through the C ABI into ``o`` (and ``lse``, (heads, total_q) fp32, if given); returns the
+    workspace, which starts as 0x7f bytes (nothing in it may be read before the call writes it). With ``status`` (a
+    list) the device planner's status word is appended to it (karpo_attn_device_status)."""
     lib = _lib.load()
     a = ops._args(q, k, v, o, q_cu, k_cu, q_cu.numel() - 1, max_q, scale, left, right, spans,
-                  plan.tensor if plan is not None else None, list(plan.header) if plan is not None else None)
+                  plan.tensor if plan is not None else None, list(plan.header) if plan is not None else None,
+                  gate=gate)
+    if lse is not None:
+        a.lse = lse.data_ptr()
     need = ctypes.c_size_t()
     _lib.check(lib.karpo_attn_workspace_bytes(ctypes.byref(a), ctypes.byref(need)), "workspace")
-    ws = torch.zeros(need.value, dtype=torch.uint8, device=q.device)
+    ws = torch.full((need.value,), 0x7F, dtype=torch.uint8, device=q.device)
     a.workspace, a.workspace_bytes = ws.data_ptr(), need.value
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     _lib.check(lib.karpo_attn_fwd(ctypes.byref(a), stream), "fwd")
@@ -424,6 +428,53 @@ def test_every_row_is_written_and_device_plan_matches_host_plan(gpu):
     o2 = torch.empty_like(w.query)
     _c_abi_call(w.query, w.key, w.value, o2, q_cu, q_cu, max_q, w.scale, -1, 0, plan=plan)
     assert torch.equal(o, o2)
+
+
+@pytest.mark.parametrize("heads,kv_heads,head,max_q,decode,shape", [
+    (8, 2, 128, 6000, False, 0), (8, 2, 128, 4096, False, 2), (8, 2, 128, 70000, False, 3), (8, 2, 128, 1, True, 1),
+    (8, 2, 64, 6000, False, 0), (8, 2, 64, 1, True, 1), (8, 2, 256, 9000, False, 0), (8, 2, 256, 4096, False, 2),
+    (8, 2, 256, 1, True, 1), (8, 2, 512, 6000, False, 0), (8, 2, 512, 1, True, 1)])
+def test_split_tiles_device_plan_matches_host_plan(gpu, heads, kv_heads, head, max_q, decode, shape):
+    """Split tiles in every tile shape that stores partials: the device planner's work list (planned into a workspace
+    that starts as garbage) is the host planner's, so the output with its LSE, and the gated output (the C ABI takes
+    no LSE with a gate), are the same bits either way, with every row written. Causal packs with one long sequence
+    (its last tiles split), or decode-shaped ones (one query per sequence over many keys: the key steps split)."""
+    if decode:
+        q_lens, k_lens, left, right = [1] * 6, [24000, 9000, 3000, 700, 40, 0], -1, -1
+    else:
+        q_lens = [min(max_q, 2000), 300, 40, 0, 7]
+        k_lens, left, right = q_lens, -1, 0
+    cu_q, cu_k = _lengths_cu(q_lens), _lengths_cu(k_lens)
+    assert _lib.kernel_shape(heads, kv_heads, head, max_q) == shape
+    g = torch.Generator(device="cpu").manual_seed(head + max_q)
+    q = torch.randn(cu_q[-1], heads, head, generator=g).to(torch.bfloat16).to(gpu)
+    k, v = (torch.randn(cu_k[-1], kv_heads, head, generator=g).to(torch.bfloat16).to(gpu) for _ in range(2))
+    gate = torch.randn(cu_q[-1], heads, head, generator=g).to(torch.bfloat16).to(gpu)
+    q_cu = torch.tensor(cu_q, dtype=torch.int32, device=gpu)
+    k_cu = torch.tensor(cu_k, dtype=torch.int32, device=gpu)
+    plan = ops.make_plan(cu_q, cu_k, heads, kv_heads, head, left, right, device=gpu, max_q=max_q)
+    assert plan.header[4] > 0, "expected split tiles in this pack"
+    outs = []
+    for use_plan in (None, plan):
+        for use_gate in (None, gate):
+            o = torch.full_like(q, float("nan"))
+            lse = torch.full((heads, cu_q[-1]), float("nan") if use_gate is None else 0.0, dtype=torch.float32,
+                             device=gpu)
+            ws = _c_abi_call(q, k, v, o, q_cu, k_cu, max_q, head ** -0.5, left, right, plan=use_plan, gate=use_gate,
+                             lse=lse if use_gate is None else None)
+            if use_plan is None:
+                dev_header, dev_merges, _ = _plan_parts(ws.view(torch.int32)[: plan.tensor.numel()])
+                assert dev_header == list(plan.header) and dev_merges == _plan_parts(plan.tensor)[1]
+            assert not torch.isnan(o).any() and not torch.isnan(lse).any()
+            outs.append((o, lse))
+    for (o_dev, lse_dev), (o_host, lse_host) in zip(outs[:2], outs[2:]):
+        assert torch.equal(o_dev, o_host) and torch.equal(lse_dev, lse_host)
+    assert not torch.equal(outs[0][0], outs[1][0])  # the gate applied
+    # the longest sequence against the oracle (its tiles are the split ones)
+    a, b = cu_q[1] - cu_q[0], cu_k[1] - cu_k[0]
+    if not decode:
+        want = oa.packed_attention(q[:a].cpu(), k[:b].cpu(), v[:b].cpu(), [0, a], [0, b], head ** -0.5, left, right)
+        assert_close(outs[0][0][:a], want, f"split tiles: D={head} max_q {max_q} shape {shape}")
 
 
 @pytest.mark.parametrize("n_seq", [1024, 1025, 6000])
