@@ -160,7 +160,8 @@ int karpo_attn_norm_rope(const KarpoNormRopeArgs* args, void* stream);
  * P = exp(scale * q.k - lse) over the visible keys and dS = P * (d_o . v - rowsum(d_o * o)). Head sizes 64, 128,
  * 256 and 512; no plan, no row table, no prologue or gate in fwd (their gradients are other ops'). Gradient tensors
  * are bf16 with head_dim contiguous; every row inside the sequences' bounds (q_cu, k_cu) is written, rows outside
- * them are not. Deterministic: a key/value head's gradients sum over its query heads in a fixed order (no atomics). */
+ * them are not. Deterministic: a key/value head's gradients sum over its query heads, and the parts of a key tile the
+ * device planner splits over its query rows (head sizes 64, 128) in part order, each in a fixed order (no atomics). */
 typedef struct KarpoAttnBwdArgs {
   KarpoAttnArgs fwd;            /* the forward call's arguments (o = its output); fwd.total_k = rows of k and v;
                                    fwd.workspace / workspace_bytes: karpo_attn_bwd_workspace_bytes of these args */

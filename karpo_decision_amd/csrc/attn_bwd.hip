@@ -6,7 +6,8 @@
 //   dV = P^T dO,  dP = dO V^T,  dS = P * (dP - D),  dQ = scale * dS K,  dK = scale * dS^T Q.
 // P and dS enter the MFMAs as bf16 (as P does in the forward), every product accumulates in fp32.
 //
-// Two kernels after the planner (plan_kernel of attn_fwd.hip: both work lists in one launch, no split tiles):
+// Two kernels after the planner (plan_kernel of attn_fwd.hip: both work lists in one launch; below head size 512 the
+// longest key tiles split over their query steps, their parts' fp32 dK / dV summed by bwd_merge_kernel):
 //   * bwd_dq_kernel (query-stationary, the forward's tiles): per (head, query row) first the log2-domain LSE (+inf
 //     for a row that sees no key, so its P are 0) and D = rowsum(dO * O), written for the dK / dV kernel (every
 //     vector is in exactly one query tile); then Q and dO of 32 query vectors per wave as MFMA B operands
@@ -350,6 +351,9 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::template occ_k<MODE>()) 
   if (item >= p.plan[0]) return;
   const int32_t* entry = p.plan + p.plan[6] + kItemInts * item;
   const int seg = entry[0], ktile = entry[1];
+  const int part = entry[2] & 0xffff, parts = entry[2] >> 16;
+  const int slot = entry[3];
+  if (parts > 1 && (slot < 0 || slot + part >= p.slots)) return;  // a partial slot outside the workspace
   const int keys_per_tile = p.plan[1];
   const int qa = p.q_cu[seg], lq = p.q_cu[seg + 1] - qa;
   const int ka = p.k_cu[seg], lk = p.k_cu[seg + 1] - ka;
@@ -430,7 +434,10 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::template occ_k<MODE>()) 
   qhi = __builtin_amdgcn_readfirstlane(qhi);
   const int r_first = qlo < qhi ? (qlo / BQ) * BQ : 0;
   const int n_rsteps = qlo < qhi ? (qhi - r_first + BQ - 1) / BQ : 0;
-  const int n_steps = n_rsteps * p.group;  // every head of the group in turn
+  const int all_steps = n_rsteps * p.group;  // every head of the group in turn
+  // a part of a split tile: steps [s_begin, s_begin + n_steps) of that sequence
+  const int s_begin = parts > 1 ? (int)((int64_t)part * all_steps / parts) : 0;
+  const int n_steps = parts > 1 ? (int)((int64_t)(part + 1) * all_steps / parts) - s_begin : all_steps;
 
   // dV alone reads dO only transposed: it keeps the transposed-read layout, whose copy reads whole rows (the S
   // layout's reads 64 bytes of each of 16 rows per instruction)
@@ -453,10 +460,12 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::template occ_k<MODE>()) 
   const int64_t q_step = (int64_t)BQ * p.sq_t, o_step = (int64_t)BQ * p.sdo_t;
   const int64_t q_wrap = p.sq_h + n_rsteps * q_step, o_wrap = p.sdo_h + n_rsteps * o_step;
   const int64_t st_wrap = 2 * p.total_q + (int64_t)n_rsteps * BQ;
-  int c_r0 = r_last;
-  const uint16_t* c_q = p.q + (int64_t)(qa + r_last) * p.sq_t + (int64_t)h0 * p.sq_h;
-  const uint16_t* c_o = p.dout + (int64_t)(qa + r_last) * p.sdo_t + (int64_t)h0 * p.sdo_h;
-  const float* c_st = p.stats + (int64_t)h0 * 2 * p.total_q + qa + r_last;
+  const int h_begin = n_rsteps > 0 ? s_begin / n_rsteps : 0;   // the first step's head (of the group) and row
+  const int r_begin = r_last - (s_begin - h_begin * n_rsteps) * BQ;
+  int c_r0 = r_begin;
+  const uint16_t* c_q = p.q + (int64_t)(qa + r_begin) * p.sq_t + (int64_t)(h0 + h_begin) * p.sq_h;
+  const uint16_t* c_o = p.dout + (int64_t)(qa + r_begin) * p.sdo_t + (int64_t)(h0 + h_begin) * p.sdo_h;
+  const float* c_st = p.stats + (int64_t)(h0 + h_begin) * 2 * p.total_q + qa + r_begin;
   auto copy_step = [&](KA_LDS char* tqk, KA_LDS char* tok, KA_LDS float* tst) {
     const int rows = min(lq - c_r0, BQ);
     const uint16_t* qs = c_q;
@@ -505,7 +514,7 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::template occ_k<MODE>()) 
   KA_LDS char* const tok1 = (KA_LDS char*)ok1;
   KA_LDS float* const tst0 = (KA_LDS float*)sts0;
   KA_LDS float* const tst1 = (KA_LDS float*)sts1;
-  int r_cur = r_last;
+  int r_cur = r_begin;
   if (n_steps > 0) copy_step(tqk0, tok0, tst0);
   wait_vmcnt<0>();
   __syncthreads();
@@ -593,6 +602,22 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::template occ_k<MODE>()) 
   }
   if (s < n_steps) step(s, tqk0, tok0, tst0, tqk1, tok1, tst1);
 
+  if (D <= 128 && parts > 1) {  // one part of a split tile: fp32 dK (before the scale) and dV for bwd_merge_kernel
+    constexpr int KT = 32 * W;
+    float* base = p.partial + bwd_partial_base(slot, part, p.n_hg, kvh, KT, D) + (wave * 32 + col) * D + half * 4;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        if constexpr (DK)
+          *(float4*)(base + db * 32 + g4 * 8) = float4{dk[db][g4 * 4], dk[db][g4 * 4 + 1], dk[db][g4 * 4 + 2],
+                                                       dk[db][g4 * 4 + 3]};
+        if constexpr (DV)
+          *(float4*)(base + KT * D + db * 32 + g4 * 8) = float4{dv[db][g4 * 4], dv[db][g4 * 4 + 1],
+                                                                dv[db][g4 * 4 + 2], dv[db][g4 * 4 + 3]};
+      }
+    return;
+  }
   if (valid) {  // lane (col, half) holds d = db*32 + (j/4)*8 + half*4 + j%4 of its key
     uint16_t* kq = p.dk + (int64_t)(ka + key) * p.sdk_t + (int64_t)kvh * p.sdk_h + half * 4;
     uint16_t* vq = p.dv + (int64_t)(ka + key) * p.sdv_t + (int64_t)kvh * p.sdv_h + half * 4;
@@ -616,11 +641,58 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::template occ_k<MODE>()) 
   }
 }
 
+// ---- the split key tiles' merge: dK = scale * sum_p dK_p, dV = sum_p dV_p, summed in part order. Thread per (split
+// tile, key/value head, key, dK or dV, 4 elements of D), in a grid-stride loop over a fixed grid.
+constexpr int kBwdMergeThreads = 256;
+constexpr int kBwdMergeBlocks = 1024;
+
+template <int D>
+__global__ __launch_bounds__(kBwdMergeThreads) void bwd_merge_kernel(BwdParams p) {
+  constexpr int KT = 32 * kBwdWaves, C4 = D / 4;
+  const int64_t units = (int64_t)p.plan[4] * p.n_hg * KT * 2 * C4;
+  const int64_t stride = (int64_t)p.n_hg * KT * 2 * D;  // floats between consecutive slots
+  for (int64_t idx = (int64_t)blockIdx.x * kBwdMergeThreads + threadIdx.x; idx < units;
+       idx += (int64_t)gridDim.x * kBwdMergeThreads) {
+    const int d = (int)(idx % C4) * 4;
+    const int64_t r = idx / C4;
+    const int which = (int)(r % 2);  // 0: dK, 1: dV
+    const int key_l = (int)((r / 2) % KT);
+    const int64_t mh = r / (2 * KT);
+    const int merge = (int)(mh / p.n_hg), kvh = (int)(mh - (int64_t)merge * p.n_hg);
+    const int32_t* e = p.plan + kPlanHeader + kMergeInts * merge;
+    const int seg = e[0], tile = e[1], parts = e[2], slot = e[3];
+    if (slot < 0 || parts < 2 || slot + parts > p.slots) continue;
+    const int ka = p.k_cu[seg], lk = p.k_cu[seg + 1] - ka;
+    const int key = tile * p.plan[1] + key_l;
+    if (key >= lk) continue;
+    const float* x = p.partial + bwd_partial_base(slot, 0, p.n_hg, kvh, KT, D) + which * KT * D + key_l * D + d;
+    float4 sum = *(const float4*)x;
+    for (int q = 1; q < parts; ++q) {
+      const float4 y = *(const float4*)(x + q * stride);
+      sum.x += y.x;
+      sum.y += y.y;
+      sum.z += y.z;
+      sum.w += y.w;
+    }
+    u32x2 out;
+    if (which == 0) {
+      out[0] = pack_bf16(sum.x * p.scale, sum.y * p.scale);
+      out[1] = pack_bf16(sum.z * p.scale, sum.w * p.scale);
+      *(u32x2*)(p.dk + (int64_t)(ka + key) * p.sdk_t + (int64_t)kvh * p.sdk_h + d) = out;
+    } else {
+      out[0] = pack_bf16(sum.x, sum.y);
+      out[1] = pack_bf16(sum.z, sum.w);
+      *(u32x2*)(p.dv + (int64_t)(ka + key) * p.sdv_t + (int64_t)kvh * p.sdv_h + d) = out;
+    }
+  }
+}
+
 // ---- launch
 
 template <int D>
 static hipError_t launch_bwd_d(const BwdParams& p, const Geometry& gq, const Geometry& gk, int32_t* plan_q,
-                               int32_t* plan_k, int64_t items_q, int64_t items_k, hipStream_t stream) {
+                               int32_t* plan_k, int64_t items_q, int64_t items_k, int64_t tiles_k, int merges_k,
+                               hipStream_t stream) {
   // the rows' statistics come from the dQ kernel (no separate pass below head size 512)
   hipError_t e;
   BwdParams pq = p;
@@ -638,7 +710,7 @@ static hipError_t launch_bwd_d(const BwdParams& p, const Geometry& gq, const Geo
   pk.n_hg = gk.n_hg;
   const dim3 grid((unsigned)(items_k * gk.n_hg));
   if (items_k > 0) {
-    if (D == 128 && items_k * gk.n_hg >= kSplitKeyTiles) {
+    if (D == 128 && tiles_k * gk.n_hg >= kSplitKeyTiles) {
       if constexpr (D == 128) {
         hipLaunchKernelGGL((bwd_dkdv_kernel<D, 1>), grid, dim3(64 * kBwdWaves), 0, stream, pk);
         hipLaunchKernelGGL((bwd_dkdv_kernel<D, 2>), grid, dim3(64 * kBwdWaves), 0, stream, pk);
@@ -647,6 +719,12 @@ static hipError_t launch_bwd_d(const BwdParams& p, const Geometry& gq, const Geo
       hipLaunchKernelGGL((bwd_dkdv_kernel<D, 3>), grid, dim3(64 * kBwdWaves), 0, stream, pk);
     }
   }
+  e = hipGetLastError();
+  if (D > 128 || e != hipSuccess || items_k <= 0 || merges_k <= 0) return e;
+  const int64_t blocks = ((int64_t)merges_k * gk.n_hg * 32 * kBwdWaves * 2 * (D / 4) + kBwdMergeThreads - 1) /
+                         kBwdMergeThreads;
+  hipLaunchKernelGGL(bwd_merge_kernel<D>, dim3((unsigned)(blocks < kBwdMergeBlocks ? blocks : kBwdMergeBlocks)),
+                     dim3(kBwdMergeThreads), 0, stream, pk);
   return hipGetLastError();
 }
 
@@ -660,9 +738,9 @@ hipError_t launch_bwd(const BwdParams& p, int head_dim, const Geometry& gq, cons
   hipError_t e = launch_plan(jobs, 2, n_seq, stream);
   if (e != hipSuccess) return e;
   switch (head_dim) {
-    case 64: return launch_bwd_d<64>(p, gq, gk, plan_q, plan_k, items_q, items_k, stream);
-    case 128: return launch_bwd_d<128>(p, gq, gk, plan_q, plan_k, items_q, items_k, stream);
-    case 256: return launch_bwd_d<256>(p, gq, gk, plan_q, plan_k, items_q, items_k, stream);
+    case 64: return launch_bwd_d<64>(p, gq, gk, plan_q, plan_k, items_q, items_k, tiles_k, merges_k, stream);
+    case 128: return launch_bwd_d<128>(p, gq, gk, plan_q, plan_k, items_q, items_k, tiles_k, merges_k, stream);
+    case 256: return launch_bwd_d<256>(p, gq, gk, plan_q, plan_k, items_q, items_k, tiles_k, merges_k, stream);
     case 512: {
       const int64_t vectors = p.total_q * p.heads;  // one vector per wave of the statistics pass
       const int64_t blocks = vectors < 4 * 8192 ? (vectors + 3) / 4 : 8192;

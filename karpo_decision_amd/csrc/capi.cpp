@@ -301,23 +301,31 @@ extern "C" int karpo_attn_norm_rope(const KarpoNormRopeArgs* a, void* stream) {
 
 namespace {
 
-// The backward's workspace: per-row stats, then the query-tile and key-tile plans, then the planners' tile bases.
+// The backward's workspace: per-row stats, then the query-tile and key-tile plans (the key tiles' with their split
+// tiles), then the planners' tile bases, then the split key tiles' fp32 partials.
 struct BwdSizes {
-  int64_t tiles_q, tiles_k, stats_bytes, plan_q, plan_k, bytes;  // plan_q / plan_k: int offsets from the stats end
+  int64_t tiles_q, tiles_k, items_k, merges_k, stats_bytes, plan_q, plan_k, tile_bases, partial_offset, bytes;
+  // plan_q / plan_k / tile_bases: int offsets from the stats end
 };
 
 BwdSizes bwd_sizes_of(const KarpoAttnBwdArgs* b) {
   const KarpoAttnArgs* a = &b->fwd;
   const Geometry gq = bwd_geometry(a->heads, a->kv_heads, a->head_dim, false);
+  const Geometry gk = bwd_geometry(a->heads, a->kv_heads, a->head_dim, true);
   BwdSizes z;
   z.tiles_q = tile_capacity(a, gq);
   const int keys = bwd_tile_vectors(a->head_dim, true);
   z.tiles_k = (a->total_k + keys - 1) / keys + a->n_seq;
+  z.items_k = z.tiles_k + split_slots(gk);
+  z.merges_k = ka_min(z.tiles_k, split_tiles(gk));
   z.stats_bytes = ((int64_t)a->heads * 2 * a->total_q * 4 + 255) / 256 * 256;
   z.plan_q = 0;
   z.plan_k = kPlanHeader + kItemInts * z.tiles_q;
-  const int64_t ints = z.plan_k + kPlanHeader + kItemInts * z.tiles_k + 2 * ((int64_t)a->n_seq + 1);  // 2 tile bases
-  z.bytes = z.stats_bytes + (ints * 4 + 255) / 256 * 256;
+  z.tile_bases = z.plan_k + kPlanHeader + kMergeInts * z.merges_k + kItemInts * z.items_k;
+  const int64_t ints = z.tile_bases + 2 * ((int64_t)a->n_seq + 1);  // 2 tile bases
+  z.partial_offset = z.stats_bytes + (ints * 4 + 255) / 256 * 256;
+  const int64_t partial = split_slots(gk) * gk.n_hg * (int64_t)keys * 2 * a->head_dim * 4;
+  z.bytes = z.partial_offset + (partial + 255) / 256 * 256;
   return z;
 }
 
@@ -373,8 +381,8 @@ extern "C" int karpo_attn_bwd(const KarpoAttnBwdArgs* b, void* stream) {
   const BwdSizes z = bwd_sizes_of(b);
   const Geometry gq = bwd_geometry(a->heads, a->kv_heads, a->head_dim, false);
   const Geometry gk = bwd_geometry(a->heads, a->kv_heads, a->head_dim, true);
-  if (z.tiles_q * gq.n_hg > (int64_t)INT32_MAX || z.tiles_k * gk.n_hg > (int64_t)INT32_MAX ||
-      z.plan_k + kPlanHeader + kItemInts * z.tiles_k > (int64_t)INT32_MAX)
+  if (z.tiles_q * gq.n_hg > (int64_t)INT32_MAX || z.items_k * gk.n_hg > (int64_t)INT32_MAX ||
+      z.tile_bases > (int64_t)INT32_MAX)
     return KARPO_ATTN_ERR_ARG;
   if (a->workspace == nullptr || a->workspace_bytes < (size_t)z.bytes || !aligned16(a->workspace))
     return KARPO_ATTN_ERR_WORKSPACE;
@@ -420,9 +428,11 @@ extern "C" int karpo_attn_bwd(const KarpoAttnBwdArgs* b, void* stream) {
   p.right = a->window_right;
   p.c = a->scale * 1.4426950408889634f;
   p.scale = a->scale;
-  int32_t* const tile_base = ints + z.plan_k + kPlanHeader + kItemInts * z.tiles_k;
-  if (launch_bwd(p, a->head_dim, gq, gk, ints + z.plan_q, ints + z.plan_k, z.tiles_q, z.tiles_k, (int)z.tiles_q, 0,
-                 (int)z.tiles_k, 0, tile_base, tile_base + a->n_seq + 1, a->n_seq,
+  p.partial = reinterpret_cast<float*>(ws + z.partial_offset);
+  p.slots = (int32_t)split_slots(gk);
+  int32_t* const tile_base = ints + z.tile_bases;
+  if (launch_bwd(p, a->head_dim, gq, gk, ints + z.plan_q, ints + z.plan_k, z.tiles_q, z.items_k, (int)z.tiles_q, 0,
+                 (int)z.tiles_k, (int)z.merges_k, tile_base, tile_base + a->n_seq + 1, a->n_seq,
                  static_cast<hipStream_t>(stream)) != hipSuccess)
     return KARPO_ATTN_ERR_LAUNCH;
   return KARPO_ATTN_OK;

@@ -69,10 +69,14 @@ struct BwdParams {
   int32_t left, right;
   float c;      // scale * log2(e) (signed)
   float scale;  // the logit scale (signed): dq and dk carry it
+  float* __restrict__ partial;  // split key tiles' fp32 dK / dV per part (bwd_partial_base)
+  int32_t slots;                // partial slots per key/value head the buffer holds
 };
 // Head size 512: the dQ and dK / dV kernels of wave pairs (attn_bwd_pair.hip), after the statistics pass.
 hipError_t launch_bwd_pair(const BwdParams& p, const Geometry& gq, const Geometry& gk, int32_t* plan_q,
                            int32_t* plan_k, int64_t items_q, int64_t items_k, hipStream_t stream);
+// items_q / items_k: the work lists' item capacities (the grids), tiles_q / tiles_k their tile capacities, merges_k
+// the key tiles' split capacity.
 hipError_t launch_bwd(const BwdParams& p, int head_dim, const Geometry& gq, const Geometry& gk, int32_t* plan_q,
                       int32_t* plan_k, int64_t items_q, int64_t items_k, int tiles_q, int merges_q, int tiles_k,
                       int merges_k, int32_t* tile_base_q, int32_t* tile_base_k, int n_seq, hipStream_t stream);

@@ -186,7 +186,10 @@ KA_HD inline FwdSizes fwd_sizes(int64_t total_q, int n_seq, int64_t max_q, int h
   return z;
 }
 
-// Backward tiles (attn_bwd.hip), never split (conc 1 makes the split length the whole pack):
+// Backward tiles (attn_bwd.hip). Query tiles never split (conc 1 makes the split length the whole pack); key tiles at
+// head sizes 64 and 128 split like the forward's, planned one per CU (the dK / dV kernel's residency at one wave per
+// SIMD), their parts' fp32 partials summed by bwd_merge_kernel (at 256 the kernel's one wave per SIMD has no
+// registers left for the partials' store path):
 //   * dkdv kernel: four waves of 32 keys, 32 query rows per step;
 //   * dq kernel: four waves of 32 query vectors, 32 keys per step (eight waves with 64-key steps, which the kernel
 //     also takes up to head size 128, measured no faster: the step's fixed costs are not what bounds it).
@@ -216,8 +219,14 @@ KA_HD inline Geometry bwd_geometry(int heads, int kv_heads, int head_dim, bool k
   g.ng = key_tiles ? 1 : (g.vectors % group == 0 ? group : 1);
   g.rows = g.vectors / g.ng;
   g.n_hg = key_tiles ? kv_heads : heads / g.ng;
-  g.conc = 1;
+  g.conc = key_tiles && head_dim <= 128 ? kComputeUnits : 1;
   return g;
+}
+
+// Floats from the backward's partial buffer to part `part` of the split key tile whose parts start at slot `slot`,
+// key/value head kvh: per slot and head dK [keys][head_dim] (before the logit scale), then dV [keys][head_dim].
+KA_HD inline int64_t bwd_partial_base(int slot, int part, int n_hg, int kvh, int keys, int head_dim) {
+  return ((int64_t)(slot + part) * n_hg + kvh) * (int64_t)keys * 2 * head_dim;
 }
 
 }  // namespace karpo

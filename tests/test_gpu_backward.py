@@ -171,6 +171,47 @@ def test_backward_is_deterministic(gpu):
         assert torch.equal(x, y)
 
 
+def test_long_key_tiles_split_over_their_query_steps(gpu, monkeypatch):
+    """One long causal sequence among short ones: the device planner splits its first key tiles over their query
+    steps (each part of the dK / dV kernel stores fp32 partials, bwd_merge_kernel sums them in part order). The key
+    tiles' plan in the workspace (which starts as garbage) lists split tiles; the gradients match the oracle and
+    repeated calls are bitwise equal."""
+    seen = []
+    real = ops._workspace
+
+    def capture(lib, fn, args, device):
+        ws = real(lib, fn, args, device)
+        if fn.__name__ == "karpo_attn_bwd_workspace_bytes":
+            ws.fill_(0x7F)
+            seen.append(ws)
+        return ws
+
+    monkeypatch.setattr(ops, "_workspace", capture)
+    q_lens, heads, kv_heads, d = [2000, 100, 37], 8, 2, 128
+    q, k, v, do, q_cu, k_cu, spans = make_pack(q_lens, q_lens, heads, kv_heads, d, seed=41)
+    got = kernel_grads(q, k, v, do, q_cu, k_cu, d ** -0.5, -1, 0, spans)
+    # the workspace: per-row stats ([heads][2][total_q] fp32, 256-byte aligned), the query tiles' plan (header, then
+    # 4 ints per tile of the capacity: 128 vectors per tile, 128 / group rows), then the key tiles' plan
+    ws = seen[-1].view(torch.int32).cpu()
+    total_q, n_seq, group = sum(q_lens), len(q_lens), heads // kv_heads
+    rows = 128 // (group if 128 % group == 0 else 1)
+    tiles_q = min(-(-total_q // rows) + n_seq, n_seq * -(-max(q_lens) // rows))
+    plan_k = -(-(heads * 2 * total_q * 4) // 256) * 256 // 4 + 12 + 4 * tiles_q
+    header = ws[plan_k: plan_k + 12].tolist()
+    assert header[1] == 128 and header[2] == 32 and header[5] == 4, header  # keys per tile, rows per step, waves
+    assert header[4] > 0, "expected split key tiles"
+    merges = ws[plan_k + 12: plan_k + 12 + 4 * header[4]].view(-1, 4).tolist()
+    assert all(seg == 0 and parts >= 2 for seg, _, parts, _ in merges)  # the long sequence's tiles
+    want = oa.packed_grads(q, k, v, do, q_cu, k_cu, d ** -0.5, -1, 0, spans, dtype=torch.float32)
+    for name, x, w in zip(("out", "dq", "dk", "dv"), got, want):
+        r = rel(x, w)
+        print(name, f"rel {r:.2e}", flush=True)
+        assert r < REL_FRO, (name, r)
+    again = kernel_grads(q, k, v, do, q_cu, k_cu, d ** -0.5, -1, 0, spans)
+    for x, y in zip(got, again):
+        assert torch.equal(x, y)
+
+
 def test_backward_refuses_what_it_does_not_take(gpu):
     dev = torch.device("cuda")
     cu = torch.tensor([0, 8], dtype=torch.int32, device=dev)

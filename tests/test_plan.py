@@ -329,8 +329,15 @@ def test_bwd_workspace_holds_stats_and_both_plans():
     stats = 4 * 2 * 1000 * 4  # [heads][2][total_q] fp32
     tiles_q = min(-(-1000 // 64) + 3, 3 * -(-600 // 64))  # 128 vectors of 2 heads: 64 rows per query tile
     tiles_k = -(-1500 // 128) + 3
-    # both plans, and a tile-base array of n_seq + 1 ints per plan (the two are built by one launch, side by side)
-    assert size.value >= stats + 4 * (8 + 4 * tiles_q + 8 + 4 * tiles_k + 2 * 4) and size.value % 256 == 0
+    # key tiles split over their query steps: parts in at most 2 x 256 / kv_heads slots per key/value head, each
+    # holding fp32 dK and dV of 128 keys
+    slots = 2 * 256 // 2
+    items_k, merges_k = tiles_k + slots, min(tiles_k, slots // 2)
+    partials = slots * 2 * 128 * 2 * 64 * 4
+    # both plans (the key tiles' with their split tiles), and a tile-base array of n_seq + 1 ints per plan (the two
+    # are built by one launch, side by side), then the partials
+    ints = 12 + 4 * tiles_q + 12 + 4 * merges_k + 4 * items_k + 2 * 4
+    assert size.value >= stats + 4 * ints + partials and size.value % 256 == 0
     assert lib.karpo_attn_bwd(ctypes.byref(_bwd_args(_args(total_q=0, total_k=100))), None) == 0  # nothing to do
 
 
