@@ -96,10 +96,16 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// One 16-byte chunk per lane from `base + voff` (bounds-checked against `bytes`: zeros past it) to `lds + 16 * lane`.
+// Cache policy of a copy whose rows no other workgroup reads again (the instruction's nt bit: streamed through the
+// caches). Only for such data: where other tiles re-read the rows from L2, it costs 7-24% (32k, 131k, Qwen layers).
+constexpr int kCopyStream = 2;
+
+// One 16-byte chunk per lane from `base + voff` (bounds-checked against `bytes`: zeros past it) to `lds + 16 * lane`,
+// with cache policy AUX (0, or kCopyStream).
+template <int AUX = 0>
 __device__ __forceinline__ void dma_16b(const uint16_t* base, int bytes, KA_LDS char* lds, uint32_t voff) {
   const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, bytes, kBufferFlags);
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (KA_LDS void*)lds, 16, voff, 0, 0, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (KA_LDS void*)lds, 16, voff, 0, 0, AUX);
 }
 
 
