@@ -171,11 +171,13 @@ def test_backward_is_deterministic(gpu):
         assert torch.equal(x, y)
 
 
-def test_long_key_tiles_split_over_their_query_steps(gpu, monkeypatch):
+@pytest.mark.parametrize("q_lens", [[2000, 100, 37], [3000] + [1] * 260], ids=["one-launch", "two-launch"])
+def test_long_key_tiles_split_over_their_query_steps(gpu, monkeypatch, q_lens):
     """One long causal sequence among short ones: the device planner splits its first key tiles over their query
     steps (each part of the dK / dV kernel stores fp32 partials, bwd_merge_kernel sums them in part order). The key
     tiles' plan in the workspace (which starts as garbage) lists split tiles; the gradients match the oracle and
-    repeated calls are bitwise equal."""
+    repeated calls are bitwise equal. With 260 one-token sequences beside it the key tiles number 2,296 workgroups of
+    capacity (8 key/value heads), so dK and dV run as two launches, each storing its own half of the partials."""
     seen = []
     real = ops._workspace
 
@@ -187,7 +189,7 @@ def test_long_key_tiles_split_over_their_query_steps(gpu, monkeypatch):
         return ws
 
     monkeypatch.setattr(ops, "_workspace", capture)
-    q_lens, heads, kv_heads, d = [2000, 100, 37], 8, 2, 128
+    heads, kv_heads, d = (8, 2, 128) if len(q_lens) < 10 else (16, 8, 128)
     q, k, v, do, q_cu, k_cu, spans = make_pack(q_lens, q_lens, heads, kv_heads, d, seed=41)
     got = kernel_grads(q, k, v, do, q_cu, k_cu, d ** -0.5, -1, 0, spans)
     # the workspace: per-row stats ([heads][2][total_q] fp32, 256-byte aligned), the query tiles' plan (header, then
@@ -202,6 +204,8 @@ def test_long_key_tiles_split_over_their_query_steps(gpu, monkeypatch):
     assert header[4] > 0, "expected split key tiles"
     merges = ws[plan_k + 12: plan_k + 12 + 4 * header[4]].view(-1, 4).tolist()
     assert all(seg == 0 and parts >= 2 for seg, _, parts, _ in merges)  # the long sequence's tiles
+    tiles_k = -(-sum(q_lens) // 128) + n_seq
+    assert (tiles_k * kv_heads >= 2048) == (len(q_lens) > 10)  # the two-launch path's threshold
     want = oa.packed_grads(q, k, v, do, q_cu, k_cu, d ** -0.5, -1, 0, spans, dtype=torch.float32)
     for name, x, w in zip(("out", "dq", "dk", "dv"), got, want):
         r = rel(x, w)
