@@ -6,8 +6,8 @@
 //   dV = P^T dO,  dP = dO V^T,  dS = P * (dP - D),  dQ = scale * dS K,  dK = scale * dS^T Q.
 // P and dS enter the MFMAs as bf16 (as P does in the forward), every product accumulates in fp32.
 //
-// Two kernels after the planner (plan_kernel of attn_fwd.hip: both work lists in one launch; below head size 512 the
-// longest key tiles split over their query steps, their parts' fp32 dK / dV summed by bwd_merge_kernel):
+// Two kernels after the planner (plan_kernel of attn_fwd.hip: both work lists in one launch; at head sizes 64 and 128
+// the longest key tiles split over their query steps, their parts' fp32 dK / dV summed by bwd_merge_kernel):
 //   * bwd_dq_kernel (query-stationary, the forward's tiles): per (head, query row) first the log2-domain LSE (+inf
 //     for a row that sees no key, so its P are 0) and D = rowsum(dO * O), written for the dK / dV kernel (every
 //     vector is in exactly one query tile); then Q and dO of 32 query vectors per wave as MFMA B operands
