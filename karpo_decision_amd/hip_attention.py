@@ -41,16 +41,21 @@ def attend(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, q_cu: to
            max_q: int, scale: float, *, causal: bool = False, window: int = -1, spans: torch.Tensor | None = None,
            plan: ops.Plan | None = None, rows: torch.Tensor | None = None, q_norm: Any = None,
            cos: torch.Tensor | None = None, sin: torch.Tensor | None = None) -> torch.Tensor:
-    """Attention per virtual sequence: (Lq, heads, D) bf16 queries over (Lk, kv heads, D) keys and values, sequence
-    i's query rows q_cu[i]:q_cu[i+1] over its key rows k_cu[i]:k_cu[i+1] (int32 on the device), ``max_q`` at least
-    its longest query range; bidirectional unless ``causal`` (aligned at each sequence's end), ``window`` keys before
-    a query's own position (-1: unbounded), ``spans`` (n, 2) int32 query-row ranges that see themselves whole;
-    ``rows`` (int32 / int64 on the device): key row r is row rows[r] of ``key`` / ``value`` (the branch gather, read
-    in place); with ``q_norm`` (a Gemma4RMSNorm module, or an ``ops.Norm``) ``query`` is q_proj's output, normalised
-    and, with ``cos`` / ``sin`` ((Lq, R) or (1, Lq, R), row i for query row i), rotated as the kernel loads it;
-    (Lq, heads, D)."""
+    """One HIP launch over every virtual sequence of the pack; returns the (Lq, heads, D) bf16 output.
+
+    ``query`` is (Lq, heads, D) bf16, ``key`` / ``value`` (Lk, kv heads, D) bf16, query head h reading key/value head
+    h // (heads / kv heads). The int32 device offsets ``q_cu`` / ``k_cu`` (n + 1 each) give virtual sequence i the
+    query rows [q_cu[i], q_cu[i + 1]) and the key rows [k_cu[i], k_cu[i + 1]); ``max_q`` bounds every sequence's
+    query count and selects the tile shape. Visible keys: the whole sequence, or with ``causal`` those up to the
+    query's own position (the last query lined up with the last key), narrowed by ``window`` (how many earlier keys
+    stay visible; -1 for all) and widened by ``spans`` ((n, 2) int32 query-row ranges, each seen whole by its own
+    rows). ``rows`` (int32 / int64 on the device) takes key row r from row rows[r] of ``key`` / ``value``, so a block
+    plan's branch gather needs no copy. With ``q_norm`` (a Gemma4RMSNorm or an ``ops.Norm``) ``query`` is q_proj's
+    raw output, which the kernel normalises while loading it, and also rotates when ``cos`` / ``sin`` are given
+    ((Lq, R) or (1, Lq, R) tables, row i for query row i)."""
     if torch.is_grad_enabled():
-        raise RuntimeError("hip_attention runs the forward only: call it under torch.inference_mode or no_grad")
+        raise RuntimeError("hip_attention.attend has no backward: call it under torch.inference_mode() or "
+                           "torch.no_grad(), or use ops.attention, which has one")
     norm = q_norm if q_norm is None or isinstance(q_norm, ops.Norm) else ops.gemma_norm(q_norm)
     rope = (cos, sin) if cos is not None else None
     return ops.run(query, key, value, q_cu, k_cu, max_q, scale, window_left=window, window_right=0 if causal else -1,
@@ -69,8 +74,9 @@ def norm(module: Any, x: torch.Tensor) -> torch.Tensor:
 
 
 def enable(model: Any, max_length: int) -> None:
-    """``attend`` as the global layers' attention of ``model`` (a ``Packed``) for sequences of up to ``max_length``
-    tokens; ValueError where it does not apply (no gfx950 GPU, a non-positive length)."""
+    """Point ``model.global_attend``, the hook a ``Packed`` model's global layers call, at ``attend`` (made causal when
+    ``model.causal_global`` is set). ``max_length``, the longest sequence the caller will pack, only has to be
+    positive: offsets are 64-bit. ValueError without a gfx950 GPU and a built library, or for max_length < 1."""
     if not supported(model.lm.embed_tokens.weight.device):
         raise ValueError("hip_attention needs an MI355X (gfx950) GPU and a built libkarpo_attn.so")
     if max_length < 1:

@@ -1,10 +1,10 @@
-"""Gemma's sliding-window layers on MI355X: causal by position, a query sees itself and the ``window`` keys before
-it, over a pack's virtual sequences with separate query and key bounds (a branch's keys are the shared block's tail,
-then its own rows; causal aligned at each sequence's end).
+"""Gemma's sliding-window attention on MI355X: each query sees its own position and the ``window`` positions before
+it, within its virtual sequence of the pack. Queries and keys carry separate bounds, so a branch sequence reads the
+shared prefix it extends followed by its own rows; positions line up at the sequences' last rows.
 
-Mirror of src/karpo_decision/families/gemma/sliding_attention.py:85-93 (``attend``); the image soft tokens'
-bidirectional spans that the reference recomputes afterwards with ``vision.see_whole`` (families/gemma/vision.py:
-198-210) are folded into the same launch through ``spans``.
+Mirror of src/karpo_decision/families/gemma/sliding_attention.py:85-93 (``attend``). The bidirectional image spans
+that the reference applies in a second pass (``vision.see_whole``, families/gemma/vision.py:198-210) are part of the
+same launch here (``spans``).
 """
 
 from __future__ import annotations
@@ -17,13 +17,14 @@ from . import ops
 def attend(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, q_cu: torch.Tensor, k_cu: torch.Tensor,
            max_q: int, max_k: int, scale: float, window: int, *, spans: torch.Tensor | None = None,
            plan: ops.Plan | None = None, rows: torch.Tensor | None = None) -> torch.Tensor:
-    """(T, heads, D) queries over (Tk, kv heads, D) keys and values (``q_cu`` / ``k_cu``: int32 boundaries), each
-    query seeing at most ``window`` keys before its own position; ``rows``: the block plan's ``s_rows`` gather read
-    in place (key row r is row rows[r] of ``key`` / ``value``); (T, heads, D).
+    """The (T, heads, D) output of (T, heads, D) queries over (Tk, kv heads, D) keys and values, the sequences
+    bounded by the int32 device offsets ``q_cu`` / ``k_cu``; a query's visible keys are its own position and the
+    ``window`` before it. ``rows`` takes key row r from row rows[r] of ``key`` / ``value`` (the block plan's
+    ``s_rows``, without a gathered copy).
 
-    Differentiable like the reference's FA4 operator pair (sliding_attention.py:36-66): when autograd needs
-    gradients the forward also keeps its log-sum-exp and the backward runs ``karpo_attn_bwd`` (keys and values as
-    tensors, not through ``rows``)."""
+    Under autograd (grad enabled and an input that requires it) the call goes through ``ops.attention``, which keeps
+    the forward's log-sum-exp and runs ``karpo_attn_bwd`` for the gradients, as the reference's FA4 operator pair
+    (sliding_attention.py:36-66) does; keys and values must then be tensors rather than read through ``rows``."""
     if window < 0:
         raise ValueError(f"a sliding window needs a non-negative left size, not {window}")
     if torch.is_grad_enabled() and any(t.requires_grad for t in (query, key, value)):
