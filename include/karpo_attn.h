@@ -120,9 +120,17 @@ typedef struct KarpoAttnArgs {
 
   /* The query the attention used, written when the fused prologue runs (its normalised, rotated bf16 vectors: the
    * reference's q after fused.norm_rope, which its backward differentiates through; a training forward keeps it).
-   * Only with q_norm or rope_cos set. */
+   * Only with q_norm or rope_cos set. It must not alias q (no byte of the two tensors' extents shared; refused
+   * with KARPO_ATTN_ERR_PROLOGUE): the parts of a split tile read q when they start, possibly after q_out is
+   * written. */
   void* q_out;                  /* device bf16 [total_q][heads][head_dim] with the strides below, or NULL */
   int64_t q_out_stride_tok, q_out_stride_head;
+
+  /* The key rows the bounds may index: rows of k and v, or with k_rows the row table's entries. Key bounds are part
+   * of the call's contract (non-decreasing from 0, k_cu[n_seq] at most this); with a value above 0 the device
+   * planner checks them like the query bounds (a violation plans nothing and leaves KARPO_ATTN_ERR_BOUNDS in the
+   * status word); 0 leaves them unchecked, the caller's guarantee. A host plan's bounds are the caller's. */
+  int64_t key_bound;
 } KarpoAttnArgs;
 
 /* Query / key normalisations of the fused prologue and of karpo_attn_norm_rope. */
@@ -193,7 +201,8 @@ int karpo_attn_plan_capacity(const KarpoAttnArgs* args, int64_t* entries);
  * triton_attention.attend's launch (triton_attention.py:103-109); the caller owns o. Every row of every head inside
  * the sequences' bounds is written: a host plan is checked against the call before anything is launched, and the
  * device planner's capacities hold for any bounds that keep the contract (non-decreasing from 0, query rows within
- * total_q, every query run at most max_q); device bounds that break it are not planned (nothing is launched past the
+ * total_q, every query run at most max_q, key rows within key_bound when it is set); device bounds that break it are
+ * not planned (nothing is launched past the
  * planner, no row is read or written) and leave KARPO_ATTN_ERR_BOUNDS in the workspace's status word. */
 int karpo_attn_fwd(const KarpoAttnArgs* args, void* stream);
 

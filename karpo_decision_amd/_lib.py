@@ -1,4 +1,4 @@
-"""ctypes binding of ``libkarpo_attn.so`` (``include/karpo_attn.h``, version 3). The library is the only compute path: if it is
+"""ctypes binding of ``libkarpo_attn.so`` (``include/karpo_attn.h``, version 4). The library is the only compute path: if it is
 missing this module raises, it never falls back to another implementation."""
 
 from __future__ import annotations
@@ -47,6 +47,7 @@ class KarpoAttnArgs(ctypes.Structure):
         ("rope_dim", ctypes.c_int32), ("gate", ctypes.c_void_p), ("gate_stride_tok", ctypes.c_int64),
         ("gate_stride_head", ctypes.c_int64), ("lse", ctypes.c_void_p),
         ("q_out", ctypes.c_void_p), ("q_out_stride_tok", ctypes.c_int64), ("q_out_stride_head", ctypes.c_int64),
+        ("key_bound", ctypes.c_int64),
     ]
 
 

@@ -1155,7 +1155,8 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanJobs jobs, int n
     int bad = 0;
     for (int i = tid; i < n_seq; i += kPlanThreads) {
       const int q0 = q_cu[i], q1 = q_cu[i + 1], k0 = k_cu[i], k1 = k_cu[i + 1];
-      bad |= q0 < 0 || k0 < 0 || q1 < q0 || k1 < k0 || q1 - q0 > job.max_q || (int64_t)q1 > job.total_q;
+      bad |= q0 < 0 || k0 < 0 || q1 < q0 || k1 < k0 || q1 - q0 > job.max_q || (int64_t)q1 > job.total_q ||
+             (job.key_bound > 0 && (int64_t)k1 > job.key_bound);
     }
     int total;
     block_exclusive_scan(bad, &total, scratch);

@@ -22,7 +22,7 @@ int check_shape(const KarpoAttnArgs* a) {
   if (a->heads < 1 || a->kv_heads < 1 || a->heads % a->kv_heads != 0) return KARPO_ATTN_ERR_HEADS;
   if (!head_dim_supported(a->head_dim)) return KARPO_ATTN_ERR_HEAD_DIM;
   if (a->window_left < -1 || a->window_right < -1) return KARPO_ATTN_ERR_WINDOW;
-  if (a->n_seq < 0 || a->total_q < 0 || a->max_q < 0) return KARPO_ATTN_ERR_ARG;
+  if (a->n_seq < 0 || a->total_q < 0 || a->max_q < 0 || a->key_bound < 0) return KARPO_ATTN_ERR_ARG;
   return KARPO_ATTN_OK;
 }
 
@@ -61,6 +61,18 @@ float rescale_threshold(float scale) { return fabsf(scale) >= 0.5f ? 0.f : 8.f; 
 
 bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
 
+// Bytes from the first to one past the last bf16 element of a [rows][heads][head_dim] tensor with these strides.
+uintptr_t extent_bytes(int64_t rows, int32_t heads, int32_t head_dim, int64_t s_tok, int64_t s_head) {
+  if (rows <= 0) return 0;
+  return (uintptr_t)(((rows - 1) * s_tok + (int64_t)(heads - 1) * s_head + head_dim) * 2);
+}
+
+// Whether two byte ranges [a, a + na) and [b, b + nb) share a byte.
+bool overlaps(const void* a, uintptr_t na, const void* b, uintptr_t nb) {
+  const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+  return na > 0 && nb > 0 && x < y + nb && y < x + na;
+}
+
 // The fused prologue's norm, weight and rotation table (shared by karpo_attn_fwd and karpo_attn_norm_rope).
 int check_norm_rope(int norm, const void* weight, const void* cos, const void* sin, int64_t stride, int rope_dim,
                     int head_dim) {
@@ -76,7 +88,7 @@ int check_norm_rope(int norm, const void* weight, const void* cos, const void* s
 
 }  // namespace
 
-extern "C" int karpo_attn_version(void) { return 3; }
+extern "C" int karpo_attn_version(void) { return 4; }
 
 extern "C" const char* karpo_attn_strerror(int status) {
   switch (status) {
@@ -93,11 +105,12 @@ extern "C" const char* karpo_attn_strerror(int status) {
     case KARPO_ATTN_ERR_LAUNCH: return "the HIP runtime refused a kernel launch";
     case KARPO_ATTN_ERR_ARG: return "sizes and the sequence count must be non-negative";
     case KARPO_ATTN_ERR_CAPACITY: return "the plan buffer is smaller than the plan";
-    case KARPO_ATTN_ERR_BOUNDS: return "sequence bounds must be non-negative and non-decreasing";
+    case KARPO_ATTN_ERR_BOUNDS:
+      return "sequence bounds must be non-negative and non-decreasing, within the rows they index and max_q";
     case KARPO_ATTN_ERR_PROLOGUE:
       return "unsupported fused prologue / gate: norm mode 0-3 with a 16-byte aligned weight for modes 1-2, both rope "
              "tables 16-byte aligned with a row stride that is a multiple of 8, rope_dim a multiple of 32 up to "
-             "head_dim, gate strides multiples of 4, q_out only with a prologue";
+             "head_dim, gate strides multiples of 4, q_out only with a prologue and not overlapping q";
     case KARPO_ATTN_ERR_SCRATCH:
       return "the call needs more scratch than karpo_attn_fwd_noalloc's 144 MiB (use karpo_attn_fwd with a workspace)";
     case KARPO_ATTN_ERR_PLAN:
@@ -159,6 +172,12 @@ extern "C" int karpo_attn_fwd(const KarpoAttnArgs* a, void* stream) {
   if (a->q_out != nullptr && ((a->q_norm == KARPO_NORM_NONE && a->rope_cos == nullptr) || !aligned16(a->q_out) ||
                               !check_stride(a->q_out_stride_tok) || !check_stride(a->q_out_stride_head)))
     return KARPO_ATTN_ERR_PROLOGUE;
+  // q_out must not share a byte with q: the parts of a split tile run in other workgroups and read q at their start,
+  // after part 0 may have written q_out (a query normalised and rotated twice)
+  if (a->q_out != nullptr &&
+      overlaps(a->q, extent_bytes(a->total_q, a->heads, a->head_dim, a->q_stride_tok, a->q_stride_head), a->q_out,
+               extent_bytes(a->total_q, a->heads, a->head_dim, a->q_out_stride_tok, a->q_out_stride_head)))
+    return KARPO_ATTN_ERR_PROLOGUE;
 
   const Geometry g = fwd_geometry(a);
   // a step's key rows are addressed with 32-bit byte offsets
@@ -188,7 +207,7 @@ extern "C" int karpo_attn_fwd(const KarpoAttnArgs* a, void* stream) {
     int32_t* dplan = reinterpret_cast<int32_t*>(ws);
     const PlanJob job = {a->q_cu,        a->k_cu,       g,          a->window_left, a->window_right,
                          dplan,          (int)z.tiles,  (int)z.merges, (int)z.items, dplan + z.plan_entries,
-                         dplan + z.status_offset, a->total_q, a->max_q, a->k_rows != nullptr};
+                         dplan + z.status_offset, a->total_q, a->max_q, a->k_rows != nullptr, a->key_bound};
     if (launch_plan(&job, 1, a->n_seq, s) != hipSuccess) return KARPO_ATTN_ERR_LAUNCH;
     plan = dplan;
   }

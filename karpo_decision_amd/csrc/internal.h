@@ -119,6 +119,7 @@ struct PlanJob {
   int64_t total_q;
   int32_t max_q;
   int32_t gather;    // the plan header's row-table flag
+  int64_t key_bound; // key rows the bounds may index, or 0: not checked
 };
 // The device planner: one workgroup per job (one or two), one launch.
 hipError_t launch_plan(const PlanJob* jobs, int n_jobs, int n_seq, hipStream_t stream);

@@ -31,8 +31,15 @@ int scratch_address(void** out) {
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return KARPO_ATTN_ERR_LAUNCH;
   std::lock_guard<std::mutex> hold(g_lock);
   if (g_scratch[dev] == nullptr) {
+    // the lookup loads this unit's code object on the device (once): not a stream operation, so a first call made
+    // while this thread captures a graph relaxes the thread's capture mode around it, as lazily initialising
+    // libraries do, and restores it
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    if (hipThreadExchangeStreamCaptureMode(&mode) != hipSuccess) return KARPO_ATTN_ERR_LAUNCH;
     void* ptr = nullptr;
-    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) return KARPO_ATTN_ERR_LAUNCH;
+    const hipError_t got = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (hipThreadExchangeStreamCaptureMode(&mode) != hipSuccess) return KARPO_ATTN_ERR_LAUNCH;
+    if (got != hipSuccess || ptr == nullptr) return KARPO_ATTN_ERR_LAUNCH;
     g_scratch[dev] = ptr;
   }
   *out = g_scratch[dev];
@@ -43,6 +50,14 @@ int scratch_address(void** out) {
 
 extern "C" int karpo_attn_fwd_noalloc(const KarpoAttnArgs* a, void* stream) {
   if (a == nullptr) return KARPO_ATTN_ERR_NULL;
+  if (a->plan != nullptr && a->plan_header != nullptr && a->plan_header[4] == 0) {
+    // a host plan that splits no tile needs no scratch: karpo_attn_fwd takes it without a workspace (and checks the
+    // header against the call), so no size limit applies and the array is not touched
+    KarpoAttnArgs b = *a;
+    b.workspace = nullptr;
+    b.workspace_bytes = 0;
+    return karpo_attn_fwd(&b, stream);
+  }
   size_t need = 0;
   const int st = karpo_attn_workspace_bytes(a, &need);
   if (st != KARPO_ATTN_OK) return st;

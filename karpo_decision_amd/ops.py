@@ -147,6 +147,8 @@ def _args(query: Tensor, key: Tensor, value: Tensor, out: Tensor | None, q_cu: T
         a.plan_header = (ctypes.c_int32 * len(plan_header))(*plan_header)
     if key_rows is not None:
         a.k_rows, a.total_k = key_rows.data_ptr(), key.shape[0]
+    # the rows the key bounds index (the device planner refuses bounds past them)
+    a.key_bound = key_rows.shape[0] if key_rows is not None else key.shape[0]
     a.q_norm, a.q_norm_eps = q_norm, q_norm_eps
     if q_norm_weight is not None:
         a.q_norm_weight = q_norm_weight.data_ptr()
@@ -211,6 +213,9 @@ def _attention_impl(query: Tensor, key: Tensor, value: Tensor, q_cu: Tensor, k_c
                                   or query_out.device != query.device or query_out.stride(2) != 1
                                   or (q_norm == NORM_NONE and rope_cos is None)):
         raise ValueError("query_out must be a bf16 tensor of the query's shape, with a fused prologue")
+    if query_out is not None and torch._C._is_alias_of(query_out, query):
+        # split tiles read the query after their first part may have written query_out: never the same memory
+        raise ValueError("query_out must not share storage with query (the kernel reads the query after writing it)")
     lib = _lib.load()
     out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
     if query.shape[0] == 0:

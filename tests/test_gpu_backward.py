@@ -331,3 +331,45 @@ def test_sliding_case_of_the_reference(gpu):
         r = rel(x, w)
         print("reference sliding case", name, f"rel {r:.2e}", flush=True)
         assert r < 5e-3, (name, r)
+
+
+@pytest.mark.parametrize("form", ["full", "markers"])
+def test_varlen_attn_trains_the_qwen_layer(gpu, form):
+    """varlen.varlen_attn under autograd, as torch's varlen_attn that the Qwen family binds (families/qwen/packed.py:
+    36-44) is differentiable: the Qwen full-attention layer's 8,192-token pack (16 / 8 heads, head_dim 128, causal,
+    enable_gqa, :123-124), or its markers-only form (the last query of every sequence over the sequence's keys,
+    bidirectional, :136-137). out, dq, dk, dv against autograd through the oracle by the layouts' criterion; the
+    fused prologue under autograd is refused."""
+    from karpo_decision_amd import varlen, workloads
+
+    dev = torch.device("cuda")
+    w = workloads.qwen_full(dev, seed=3)
+    q_cu, k_cu = w.q_cu, w.k_cu
+    q, k, v = w.query.cpu(), w.key.cpu(), w.value.cpu()
+    if form == "markers":
+        q = torch.stack([q[b - 1] for b in q_cu[1:]])  # one marker query per sequence
+        q_cu = list(range(len(k_cu)))
+        window, max_q = (-1, -1), 1
+    else:
+        window, max_q = (-1, 0), w.max_q
+    g = torch.Generator().manual_seed(17)
+    do = torch.randn(q.shape, generator=g).bfloat16()
+    xs = [t.to(dev).requires_grad_(True) for t in (q, k, v)]
+    qc = torch.tensor(q_cu, dtype=torch.int32, device=dev)
+    kc = torch.tensor(k_cu, dtype=torch.int32, device=dev)
+    print("varlen", form, len(k_cu) - 1, "sequences", flush=True)
+    out = varlen.varlen_attn(*xs, qc, kc, max_q, w.max_q, scale=w.scale, window_size=window, enable_gqa=True)
+    out.backward(do.to(dev))
+    torch.cuda.synchronize()
+    got = [out.detach()] + [x.grad for x in xs]
+    want = oa.packed_grads(q, k, v, do, q_cu, k_cu, w.scale, window[0], window[1], dtype=torch.float32)
+    base = oa.packed_grads(q, k, v, do, q_cu, k_cu, w.scale, window[0], window[1], dtype=torch.bfloat16)
+    for name, x, ww, b in zip(("out", "dq", "dk", "dv"), got, want, base):
+        assert torch.isfinite(x).all(), name
+        r, rb = rel(x, ww), rel(b, ww)
+        print("varlen", form, name, f"rel {r:.2e} (oracle bf16 {rb:.2e})", flush=True)
+        assert r < REL_FRO, (name, r)
+        assert r < 2 * rb + 2e-3, (name, r, rb)
+    with pytest.raises(RuntimeError, match="forward only"):
+        varlen.varlen_attn(*xs, qc, kc, max_q, w.max_q, scale=w.scale, window_size=window, enable_gqa=True,
+                           q_norm=ops.Norm(ops.NORM_PLAIN, None, 1e-6))

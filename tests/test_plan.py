@@ -30,7 +30,7 @@ def test_library_exports_every_declared_function():
     assert set(names) == set(_lib.EXPORTS)
     for name in names:
         assert hasattr(lib, name), name
-    assert lib.karpo_attn_version() == 3
+    assert lib.karpo_attn_version() == 4
 
 
 def host_plan(q_cu, k_cu, heads, kv_heads, head_dim, left, right, max_q=_lib.LONG):
@@ -476,6 +476,33 @@ def test_norm_rope_refuses_tables_that_do_not_fit():
                 ops.norm_rope(x, norm, (cos, sin))
         with pytest.raises(ValueError, match="out must"):
             ops.norm_rope(x, norm, out=torch.empty(10, 2, 64, **bf))
+
+
+def test_query_out_must_not_alias_the_query():
+    """The parts of a split tile read the query when they start, possibly after part 0 has written the prologue's
+    query to q_out: a q_out that shares a byte with q is refused (KARPO_ATTN_ERR_PROLOGUE) before any launch, by the
+    C ABI and by ops.run; a q_out of its own passes those checks."""
+    lib = _lib.load()
+    base = 1 << 24
+    weight = 1 << 23
+    # q spans (100 - 1) * 256 + 3 * 64 + 64 elements = 25,600 elements = 51,200 bytes from base
+    for q_out, refused in ((base, True), (base + 51_200 - 16, True), (base - 512, True), (base + 51_200, False),
+                           (base - 51_200, False)):
+        a = _args(q=base, q_norm=1, q_norm_weight=weight, q_norm_eps=1e-6, q_out=q_out)
+        a.q_out_stride_tok, a.q_out_stride_head = 256, 64
+        status = lib.karpo_attn_fwd(ctypes.byref(a), None)
+        assert status == (_lib.ERR_PROLOGUE if refused else 5), (q_out - base, status)  # 5: no workspace, next check
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    with FakeTensorMode():
+        bf = dict(dtype=torch.bfloat16, device="cuda")
+        q = torch.empty(10, 4, 64, **bf)
+        k = torch.empty(12, 2, 64, **bf)
+        cu = torch.empty(3, dtype=torch.int32, device="cuda")
+        norm = ops.Norm(ops.NORM_WEIGHT, torch.empty(64, **bf), 1e-6)
+        for q_out in (q, q[:], q.view(10, 4, 64)):
+            with pytest.raises(ValueError, match="must not share storage"):
+                ops.run(q, k, k, cu, cu, 8, 0.1, -1, 0, q_norm=norm, query_out=q_out)
 
 
 def test_noalloc_entry_point_refuses_calls_beyond_its_scratch():
