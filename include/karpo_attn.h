@@ -213,7 +213,10 @@ int karpo_attn_fwd(const KarpoAttnArgs* args, void* stream);
  * karpo_attn_workspace_bytes exceeds 144 MiB are refused with KARPO_ATTN_ERR_SCRATCH before anything runs. Every
  * call on one device shares that device's array (nothing in it needs to start at zero: each call's planner and
  * kernels write what they read), so calls that overlap on one device race; serialise them (one stream, or events).
- * Allocates nothing: no hipMalloc, no hipFree. */
+ * Allocates nothing: no hipMalloc, no hipFree. The first call on a device looks the array up (HIP loads it then);
+ * that call may be made while the calling thread captures a graph (it relaxes the thread's capture mode around the
+ * lookup only). A host plan that splits no tile needs no scratch: such a call runs like karpo_attn_fwd without a
+ * workspace, whatever its size. */
 int karpo_attn_fwd_noalloc(const KarpoAttnArgs* args, void* stream);
 
 /* The status word the device planner of the last karpo_attn_fwd call on this workspace (args->plan NULL) left:

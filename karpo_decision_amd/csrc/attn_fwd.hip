@@ -59,7 +59,9 @@ namespace karpo {
 template <int D, int SHAPE> struct TileCfg {
   static constexpr int W = tile_waves(D, SHAPE);
   static constexpr int BN = tile_keys(D, SHAPE);
+  static constexpr int QB = tile_blocks(D, SHAPE);  // 32-vector query blocks per wave
   static constexpr int OCC = SHAPE == kNarrow ? (D >= 256 ? 1 : 2)
+                             : SHAPE == kDual ? 2
                              : D == 512       ? 2
                              : D == 64        ? 4
                              : D == 128       ? 3
@@ -231,6 +233,7 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
   constexpr int W = TileCfg<D, SHAPE>::W;  // waves of the workgroup
   constexpr int BN = TileCfg<D, SHAPE>::BN;
   constexpr bool PAIR = TileCfg<D, SHAPE>::PAIR;
+  constexpr int QB = TileCfg<D, SHAPE>::QB;  // 32-vector query blocks per wave
   constexpr int DC = D / 16;       // 16-wide head-dim chunks of the QK^T contraction
   constexpr int DB = D / 32;       // 32-row head-dim blocks of O^T
   constexpr int QC = PAIR ? DC / 2 : DC;  // chunks of Q this wave holds (half of D in a pair)
@@ -241,6 +244,7 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
   constexpr int BLKS = TILE / 1024;               // 1 KiB DMA instructions per K or V tile
   constexpr int INSTS = (BLKS + W - 1) / W;       // per wave (the last waves may issue fewer)
   static_assert(BLKS >= 1, "a tile holds at least one DMA instruction");
+  static_assert(!PAIR || QB == 1, "a pair holds one query block");
 
   // K/V buffers: NB - 1 steps of copies in flight. One-wave tiles that stream their keys (decode-shaped packs, HBM
   // bound) keep three steps in flight in 64 KiB (two workgroups per CU: 96 KiB of copies in flight per CU instead of
@@ -296,30 +300,45 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
   const int col = lane & 31, half = lane >> 5;
   const int dh = PAIR ? (wave & 1) : 0;  // in a pair: which half of D this wave holds
 
-  // ---- this lane's query vector: position, head, visible key ranges
-  const int vec = (PAIR ? (wave >> 1) : wave) * 32 + col;
-  const int off = vec / p.ng;
-  const int pos = tile * rows_per_tile + off;
-  const int head = hg * p.ng + (vec - off * p.ng);
-  const bool valid = pos < lq;
-  int lo = 0, hi = 0, sl = 0, sh = 0;
+  // ---- this lane's query vectors (one per block): position, head, visible key ranges. With two blocks per wave the
+  // registers hold the operands and accumulators of both: the key ranges wait in LDS for the masked steps, and the
+  // vectors' rows are worked out again for the store from a copy of the lane index the compiler cannot see through
+  // (so it keeps no set-up value live across the key loop).
+  constexpr bool KEYS_IN_LDS = QB > 1;
+  __shared__ int4 keys_lds[KEYS_IN_LDS ? QB * W * 64 : 1];
+  int vec[QB], pos[QB], head[QB];
+  bool valid[QB];
+  int lo[QB], hi[QB], sl[QB], sh[QB];
+  auto lane_query = [&](int b, int column) {
+    vec[b] = lane_vector(wave, b, column, PAIR, QB);
+    const int off = vec[b] / p.ng;
+    pos[b] = tile * rows_per_tile + off;
+    head[b] = hg * p.ng + (vec[b] - off * p.ng);
+    valid[b] = pos[b] < lq;
+  };
   int wlo = INT32_MAX, whi = INT32_MIN, wflo = INT32_MIN, wfhi = INT32_MAX;
-  if (valid) {
-    const LaneKeys lk_ = lane_keys(pos, qa, lq, lk, p.left, p.right, p.spans, p.n_spans);
-    lo = lk_.lo;
-    hi = lk_.hi;
-    sl = lk_.sl;
-    sh = lk_.sh;
-    wflo = lo;
-    wfhi = hi;
-    if (lo < hi) {
-      wlo = lo;
-      whi = hi;
+#pragma unroll
+  for (int b = 0; b < QB; ++b) {
+    lane_query(b, col);
+    lo[b] = hi[b] = sl[b] = sh[b] = 0;
+    if (valid[b]) {
+      const LaneKeys lk_ = lane_keys(pos[b], qa, lq, lk, p.left, p.right, p.spans, p.n_spans);
+      lo[b] = lk_.lo;
+      hi[b] = lk_.hi;
+      sl[b] = lk_.sl;
+      sh[b] = lk_.sh;
+      wflo = max(wflo, lo[b]);
+      wfhi = min(wfhi, hi[b]);
+      if (lo[b] < hi[b]) {
+        wlo = min(wlo, lo[b]);
+        whi = max(whi, hi[b]);
+      }
+      if (sl[b] < sh[b]) {
+        wlo = min(wlo, sl[b]);
+        whi = max(whi, sh[b]);
+      }
     }
-    if (sl < sh) {
-      wlo = min(wlo, sl);
-      whi = max(whi, sh);
-    }
+    if constexpr (KEYS_IN_LDS) keys_lds[b * W * 64 + tid] = int4{lo[b], hi[b], sl[b], sh[b]};
   }
   wlo = __builtin_amdgcn_readfirstlane(wave_min(wlo));
   whi = __builtin_amdgcn_readfirstlane(wave_max(whi));
@@ -332,27 +351,31 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
     }
   }
 
-  // this wave's chunks of the query (a pair's second wave: the second half of D), with the prologue applied; loaded
-  // under the first K/V copy's latency (a pair loads them before: its norm also streams the other half's chunks)
-  bf16x8 qop[QC];
+  // this wave's chunks of its queries (a pair's second wave: the second half of D), with the prologue applied;
+  // loaded under the first K/V copy's latency (a pair loads them before: its norm also streams the other half's
+  // chunks)
+  bf16x8 qop[QB][QC];
   auto load_q = [&]() {
-    const uint16_t* qrow = p.q + (int64_t)(qa + pos) * p.sq_t + (int64_t)head * p.sq_h;
-    u32x4 x[QC];
 #pragma unroll
-    for (int i = 0; i < QC; ++i) {
-      x[i] = u32x4{0, 0, 0, 0};
-      if (valid) x[i] = *(const u32x4*)(qrow + half * 8 + (dh * QC + i) * 16);
-    }
-    if (p.q_norm != KARPO_NORM_NONE || p.rope_cos != nullptr) {
-      if (valid) query_prologue<D, QC>(p, qrow, (int64_t)(qa + pos), half, dh * QC, x);
-      if (p.q_out != nullptr && valid && part == 0) {  // the attention's query, once per (row, head)
-        uint16_t* qo = p.q_out + (int64_t)(qa + pos) * p.sqo_t + (int64_t)head * p.sqo_h + half * 8;
+    for (int b = 0; b < QB; ++b) {
+      const uint16_t* qrow = p.q + (int64_t)(qa + pos[b]) * p.sq_t + (int64_t)head[b] * p.sq_h;
+      u32x4 x[QC];
 #pragma unroll
-        for (int i = 0; i < QC; ++i) *(u32x4*)(qo + (dh * QC + i) * 16) = x[i];
+      for (int i = 0; i < QC; ++i) {
+        x[i] = u32x4{0, 0, 0, 0};
+        if (valid[b]) x[i] = *(const u32x4*)(qrow + half * 8 + (dh * QC + i) * 16);
       }
-    }
+      if (p.q_norm != KARPO_NORM_NONE || p.rope_cos != nullptr) {
+        if (valid[b]) query_prologue<D, QC>(p, qrow, (int64_t)(qa + pos[b]), half, dh * QC, x);
+        if (p.q_out != nullptr && valid[b] && part == 0) {  // the attention's query, once per (row, head)
+          uint16_t* qo = p.q_out + (int64_t)(qa + pos[b]) * p.sqo_t + (int64_t)head[b] * p.sqo_h + half * 8;
 #pragma unroll
-    for (int i = 0; i < QC; ++i) qop[i] = __builtin_bit_cast(bf16x8, x[i] ^ p.qsign);
+          for (int i = 0; i < QC; ++i) *(u32x4*)(qo + (dh * QC + i) * 16) = x[i];
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < QC; ++i) qop[b][i] = __builtin_bit_cast(bf16x8, x[i] ^ p.qsign);
+    }
   };
   if constexpr (PAIR) load_q();
   int klo = wlo, khi = whi;
@@ -454,13 +477,20 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
   const int v_read =
       v_offset<D>(8 * (g >> 1) + (jl >> 2), 16 * (g & 1) + 4 * (jl & 3)) + dh * OB * 256;  // + kc, rr, db offsets
 
-  f32x16 acc[OB];
+  f32x16 acc[QB][OB];
 #pragma unroll
-  for (int db = 0; db < OB; ++db) acc[db] = f32x16{};
+  for (int b = 0; b < QB; ++b)
+#pragma unroll
+    for (int db = 0; db < OB; ++db) acc[b][db] = f32x16{};
   // the running maximum starts finite: before the first visible key exp2(logit - m) is exp2(-inf) = 0 all the same,
   // and a rescale from it multiplies zeros (a part that sees no key stores m = -1e30 and l = 0: the merge gives it
   // weight 1 over zero sums, so an empty row still comes out 0 with LSE -inf)
-  float m = -1e30f, l = 0.f;
+  float m[QB], l[QB];
+#pragma unroll
+  for (int b = 0; b < QB; ++b) {
+    m[b] = -1e30f;
+    l[b] = 0.f;
+  }
   const float c = p.c;
   const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
 
@@ -528,16 +558,20 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
     if (GATHER && s + NB < n_steps) fetch_rows(j0 + NB * BN);
     const bool active = j0 < whi && j0 + BN > wlo;  // wave-uniform: some query of this wave sees a key of the step
     if (PAIR || active) {  // a pair enters together (its barriers), each wave computes only when active
-    f32x16 st[KB];
+    f32x16 st[QB][KB];
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) st[kb] = f32x16{};
+    for (int b = 0; b < QB; ++b)
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) st[b][kb] = f32x16{};
     if (active) {
 #pragma unroll
       for (int dc = 0; dc < QC; ++dc) {
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
           const bf16x8 a = *(const KA_LDS bf16x8*)(kt + k_read + kb * (2 * (D / 8) * 256) + dc * 512);
-          st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qop[dc], st[kb], 0, 0, 0);
+#pragma unroll
+          for (int b = 0; b < QB; ++b)  // one K operand read feeds every query block
+            st[b][kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qop[b][dc], st[b][kb], 0, 0, 0);
         }
       }
     }
@@ -550,57 +584,69 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
       if (active) {
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4)
-          slot[q4 * 64] = f32x4{st[0][4 * q4], st[0][4 * q4 + 1], st[0][4 * q4 + 2], st[0][4 * q4 + 3]};
+          slot[q4 * 64] = f32x4{st[0][0][4 * q4], st[0][0][4 * q4 + 1], st[0][0][4 * q4 + 2], st[0][0][4 * q4 + 3]};
       }
       __syncthreads();
       if (active) {
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {  // a sum of two terms: equal in both waves (addition commutes exactly)
           const f32x4 o = other[q4 * 64];
-          st[0][4 * q4] += o.x;
-          st[0][4 * q4 + 1] += o.y;
-          st[0][4 * q4 + 2] += o.z;
-          st[0][4 * q4 + 3] += o.w;
+          st[0][0][4 * q4] += o.x;
+          st[0][0][4 * q4 + 1] += o.y;
+          st[0][0][4 * q4 + 2] += o.z;
+          st[0][0][4 * q4 + 3] += o.w;
         }
       }
     }
     if (active) {
-      if (!(j0 >= wflo && j0 + BN <= wfhi)) {  // some query of this wave does not see every key of the step
+      bf16x8 pb[QB][KC];
+#pragma unroll
+      for (int b = 0; b < QB; ++b) {
+        if (!(j0 >= wflo && j0 + BN <= wfhi)) {  // some query of this wave does not see every key of the step
+          int klo_ = lo[b], khi_ = hi[b], ksl = sl[b], ksh = sh[b];
+          if constexpr (KEYS_IN_LDS) {
+            const int4 kk = keys_lds[b * W * 64 + tid];
+            klo_ = kk.x;
+            khi_ = kk.y;
+            ksl = kk.z;
+            ksh = kk.w;
+          }
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+            for (int jj = 0; jj < 16; ++jj) {
+              const int key = j0 + kb * 32 + (jj >> 3) * 16 + half * 8 + (jj & 7);
+              const bool vis = ((unsigned)(key - klo_) < (unsigned)(khi_ - klo_)) |
+                               ((unsigned)(key - ksl) < (unsigned)(ksh - ksl));
+              st[b][kb][jj] = vis ? st[b][kb][jj] : -INFINITY;
+            }
+        }
+        float mx = -INFINITY;
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-          for (int jj = 0; jj < 16; ++jj) {
-            const int key = j0 + kb * 32 + (jj >> 3) * 16 + half * 8 + (jj & 7);
-            const bool vis = ((unsigned)(key - lo) < (unsigned)(hi - lo)) | ((unsigned)(key - sl) < (unsigned)(sh - sl));
-            st[kb][jj] = vis ? st[kb][jj] : -INFINITY;
+          for (int jj = 0; jj < 16; ++jj) mx = fmaxf(mx, st[b][kb][jj]);
+        const float mt = half_swap_max(mx) * c;
+        const bool need = mt > m[b] + p.tau;
+        if (__builtin_amdgcn_ballot_w64(need)) {  // raise the running maximum (rare after the first steps)
+          const float mn = need ? mt : m[b];
+          const float alpha = need ? __builtin_amdgcn_exp2f(m[b] - mn) : 1.f;  // from the start value: alpha = 0
+          m[b] = mn;
+          l[b] *= alpha;
+#pragma unroll
+          for (int db = 0; db < OB; ++db) acc[b][db] *= alpha;
+        }
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc) {
+#pragma unroll
+          for (int t = 0; t < 8; t += 2) {
+            const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[b][kc >> 1][(kc & 1) * 8 + t], c, -m[b]));
+            const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[b][kc >> 1][(kc & 1) * 8 + t + 1], c, -m[b]));
+            const bf16x2 pr = {(__bf16)e0, (__bf16)e1};
+            pb[b][kc][t] = pr[0];
+            pb[b][kc][t + 1] = pr[1];
+            l[b] = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, l[b], false);  // l sums the bf16 P the product uses
           }
-      }
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-        for (int jj = 0; jj < 16; ++jj) mx = fmaxf(mx, st[kb][jj]);
-      const float mt = half_swap_max(mx) * c;
-      const bool need = mt > m + p.tau;
-      if (__builtin_amdgcn_ballot_w64(need)) {  // raise the running maximum (rare after the first steps)
-        const float mn = need ? mt : m;
-        const float alpha = need ? __builtin_amdgcn_exp2f(m - mn) : 1.f;  // from the start value: alpha = 0
-        m = mn;
-        l *= alpha;
-#pragma unroll
-        for (int db = 0; db < OB; ++db) acc[db] *= alpha;
-      }
-      bf16x8 pb[KC];
-#pragma unroll
-      for (int kc = 0; kc < KC; ++kc) {
-#pragma unroll
-        for (int t = 0; t < 8; t += 2) {
-          const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[kc >> 1][(kc & 1) * 8 + t], c, -m));
-          const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[kc >> 1][(kc & 1) * 8 + t + 1], c, -m));
-          const bf16x2 pr = {(__bf16)e0, (__bf16)e1};
-          pb[kc][t] = pr[0];
-          pb[kc][t + 1] = pr[1];
-          l = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, l, false);  // l sums the bf16 P the product uses
         }
       }
 #pragma unroll
@@ -614,7 +660,9 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
                 bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                             (KA_LDS s16x4*)(vt + v_read + (kc * 4 + rr) * (D / 16) * 128 + db * 256)));
           const bf16x8 a = __builtin_shufflevector(pv[0], pv[1], 0, 1, 2, 3, 4, 5, 6, 7);
-          acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[kc], acc[db], 0, 0, 0);
+#pragma unroll
+          for (int b = 0; b < QB; ++b)  // one V operand read feeds every query block
+            acc[b][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[b][kc], acc[b][db], 0, 0, 0);
         }
       }
     }
@@ -640,40 +688,50 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
       if (s + i < n_steps) step(s + i, kbuf(i), vbuf(i), kbuf((i + NB - 1) % NB), vbuf((i + NB - 1) % NB));
   }
 
-  // ---- store: lane (col, half) holds d = db*32 + (j/4)*8 + half*4 + j%4 of its query vector
-  const float lt = half_swap_sum(l);
-  if (parts > 1) {  // one part of a split tile: unnormalised fp32 O, m and l for merge_kernel
-    constexpr int V = tile_vectors(D, SHAPE);
-    float* base = p.partial + partial_base(slot, part, p.n_hg, hg, V, D);
-    float* op = base + (int64_t)vec * D + dh * (D / 2) + half * 4;
+  // ---- store: lane (col, half) holds d = db*32 + (j/4)*8 + half*4 + j%4 of its query vectors
+  if constexpr (QB > 1) {
+    int column = col;
+    asm volatile("" : "+v"(column));  // opaque: the rows below are recomputed, not kept from the set-up
 #pragma unroll
-    for (int db = 0; db < OB; ++db)
-#pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        float4 x = {acc[db][g4 * 4], acc[db][g4 * 4 + 1], acc[db][g4 * 4 + 2], acc[db][g4 * 4 + 3]};
-        *(float4*)(op + db * 32 + g4 * 8) = x;
-      }
-    if (half == 0 && dh == 0) {
-      base[V * D + vec] = m;
-      base[V * D + V + vec] = lt;
-    }
-    return;
+    for (int b = 0; b < QB; ++b) lane_query(b, column);
   }
-  const float inv = lt > 0.f ? 1.f / lt : 0.f;
-  if (valid && p.lse != nullptr && half == 0 && dh == 0)  // ln(2^m * l): m is in the log2 domain of scale * q.k
-    p.lse[(int64_t)head * p.lse_stride + qa + pos] = lt > 0.f ? (m + __log2f(lt)) * 0.69314718055994531f : -INFINITY;
-  if (valid) {
-    uint16_t* op = p.o + (int64_t)(qa + pos) * p.so_t + (int64_t)head * p.so_h + dh * (D / 2) + half * 4;
-    const uint16_t* gp = p.gate != nullptr
-                             ? p.gate + (int64_t)(qa + pos) * p.sg_t + (int64_t)head * p.sg_h + dh * (D / 2) + half * 4
-                             : nullptr;
 #pragma unroll
-    for (int db = 0; db < OB; ++db) {
+  for (int b = 0; b < QB; ++b) {
+    const float lt = half_swap_sum(l[b]);
+    if (parts > 1) {  // one part of a split tile: unnormalised fp32 O, m and l for merge_kernel
+      constexpr int V = tile_vectors(D, SHAPE);
+      float* base = p.partial + partial_base(slot, part, p.n_hg, hg, V, D);
+      float* op = base + (int64_t)vec[b] * D + dh * (D / 2) + half * 4;
 #pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        *(u32x2*)(op + db * 32 + g4 * 8) =
-            output4(acc[db][g4 * 4] * inv, acc[db][g4 * 4 + 1] * inv, acc[db][g4 * 4 + 2] * inv,
-                    acc[db][g4 * 4 + 3] * inv, gp != nullptr ? gp + db * 32 + g4 * 8 : nullptr);
+      for (int db = 0; db < OB; ++db)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          float4 x = {acc[b][db][g4 * 4], acc[b][db][g4 * 4 + 1], acc[b][db][g4 * 4 + 2], acc[b][db][g4 * 4 + 3]};
+          *(float4*)(op + db * 32 + g4 * 8) = x;
+        }
+      if (half == 0 && dh == 0) {
+        base[V * D + vec[b]] = m[b];
+        base[V * D + V + vec[b]] = lt;
+      }
+      continue;
+    }
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    if (valid[b] && p.lse != nullptr && half == 0 && dh == 0)  // ln(2^m * l): m is in the log2 domain of scale * q.k
+      p.lse[(int64_t)head[b] * p.lse_stride + qa + pos[b]] =
+          lt > 0.f ? (m[b] + __log2f(lt)) * 0.69314718055994531f : -INFINITY;
+    if (valid[b]) {
+      uint16_t* op = p.o + (int64_t)(qa + pos[b]) * p.so_t + (int64_t)head[b] * p.so_h + dh * (D / 2) + half * 4;
+      const uint16_t* gp = p.gate != nullptr ? p.gate + (int64_t)(qa + pos[b]) * p.sg_t + (int64_t)head[b] * p.sg_h +
+                                                   dh * (D / 2) + half * 4
+                                             : nullptr;
+#pragma unroll
+      for (int db = 0; db < OB; ++db) {
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          *(u32x2*)(op + db * 32 + g4 * 8) =
+              output4(acc[b][db][g4 * 4] * inv, acc[b][db][g4 * 4 + 1] * inv, acc[b][db][g4 * 4 + 2] * inv,
+                      acc[b][db][g4 * 4 + 3] * inv, gp != nullptr ? gp + db * 32 + g4 * 8 : nullptr);
+        }
       }
     }
   }
@@ -1023,9 +1081,9 @@ __global__ __launch_bounds__(512, 2) void attn_fwd_pair_pp_kernel(Params p) {
 constexpr int kMergeThreads = 256;
 constexpr int kMergeBlocks = 1024;
 
-template <int D, int W>
+template <int D, int W, int V>
 __global__ __launch_bounds__(kMergeThreads) void merge_kernel(Params p) {
-  constexpr int V = 32 * W / (D == 512 ? 2 : 1), C4 = D / 4;
+  constexpr int C4 = D / 4;
   if (p.plan[5] != W) return;
   const int64_t units = (int64_t)p.plan[4] * p.n_hg * V * C4;
   const int rows_per_tile = p.plan[1];
@@ -1353,7 +1411,9 @@ hipError_t launch_norm_rope(const NormRopeParams& p, int head_dim, hipStream_t s
 
 // Whether a shape is built with a row table: every shape but the wide and long tiles at head sizes 128 and 256,
 // which tile_shape never selects for a call with a row table.
-constexpr bool gather_built(int d, int shape) { return !((d == 128 || d == 256) && (shape == kWide || shape == kLong)); }
+constexpr bool gather_built(int d, int shape) {
+  return !((d == 128 || d == 256) && (shape == kWide || shape == kLong || shape == kDual));
+}
 
 template <int D, int SHAPE>
 static hipError_t launch_attn(const Params& p, int64_t items, int64_t merges, int n_hg, hipStream_t stream) {
@@ -1377,7 +1437,8 @@ static hipError_t launch_attn(const Params& p, int64_t items, int64_t merges, in
   if (e != hipSuccess || merges <= 0) return e;
   constexpr int64_t per_merge = (int64_t)tile_vectors(D, SHAPE) * (D / 4);  // threads of one head group
   const int64_t blocks = (merges * n_hg * per_merge + kMergeThreads - 1) / kMergeThreads;
-  hipLaunchKernelGGL((merge_kernel<D, Cfg::W>), dim3((unsigned)(blocks < kMergeBlocks ? blocks : kMergeBlocks)),
+  hipLaunchKernelGGL((merge_kernel<D, Cfg::W, tile_vectors(D, SHAPE)>),
+                     dim3((unsigned)(blocks < kMergeBlocks ? blocks : kMergeBlocks)),
                      dim3(kMergeThreads), 0, stream, p);
   return hipGetLastError();
 }
@@ -1386,18 +1447,19 @@ static hipError_t launch_attn(const Params& p, int64_t items, int64_t merges, in
 hipError_t launch_forward(const Params& p, int head_dim, const Geometry& g, int64_t items, int64_t merges,
                           hipStream_t stream) {
   if (items <= 0) return hipSuccess;
-  switch (head_dim * 4 + g.shape) {  // the shapes tile_shape selects per head size
-    case 64 * 4 + kWide: return launch_attn<64, kWide>(p, items, merges, g.n_hg, stream);
-    case 64 * 4 + kNarrow: return launch_attn<64, kNarrow>(p, items, merges, g.n_hg, stream);
-    case 128 * 4 + kWide: return launch_forward_128(p, kWide, items, merges, g.n_hg, stream);
-    case 128 * 4 + kNarrow: return launch_attn<128, kNarrow>(p, items, merges, g.n_hg, stream);
-    case 128 * 4 + kSmall: return launch_attn<128, kSmall>(p, items, merges, g.n_hg, stream);
-    case 128 * 4 + kLong: return launch_forward_128(p, kLong, items, merges, g.n_hg, stream);
-    case 256 * 4 + kWide: return launch_attn<256, kWide>(p, items, merges, g.n_hg, stream);
-    case 256 * 4 + kNarrow: return launch_attn<256, kNarrow>(p, items, merges, g.n_hg, stream);
-    case 256 * 4 + kSmall: return launch_attn<256, kSmall>(p, items, merges, g.n_hg, stream);
-    case 512 * 4 + kWide: return launch_attn<512, kWide>(p, items, merges, g.n_hg, stream);
-    case 512 * 4 + kNarrow: return launch_attn<512, kNarrow>(p, items, merges, g.n_hg, stream);
+  switch (head_dim * 8 + g.shape) {  // the shapes tile_shape selects per head size
+    case 64 * 8 + kWide: return launch_attn<64, kWide>(p, items, merges, g.n_hg, stream);
+    case 64 * 8 + kNarrow: return launch_attn<64, kNarrow>(p, items, merges, g.n_hg, stream);
+    case 128 * 8 + kWide: return launch_forward_128(p, kWide, items, merges, g.n_hg, stream);
+    case 128 * 8 + kNarrow: return launch_attn<128, kNarrow>(p, items, merges, g.n_hg, stream);
+    case 128 * 8 + kSmall: return launch_attn<128, kSmall>(p, items, merges, g.n_hg, stream);
+    case 128 * 8 + kLong: return launch_forward_128(p, kLong, items, merges, g.n_hg, stream);
+    case 128 * 8 + kDual: return launch_forward_128(p, kDual, items, merges, g.n_hg, stream);
+    case 256 * 8 + kWide: return launch_attn<256, kWide>(p, items, merges, g.n_hg, stream);
+    case 256 * 8 + kNarrow: return launch_attn<256, kNarrow>(p, items, merges, g.n_hg, stream);
+    case 256 * 8 + kSmall: return launch_attn<256, kSmall>(p, items, merges, g.n_hg, stream);
+    case 512 * 8 + kWide: return launch_attn<512, kWide>(p, items, merges, g.n_hg, stream);
+    case 512 * 8 + kNarrow: return launch_attn<512, kNarrow>(p, items, merges, g.n_hg, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -1413,6 +1475,7 @@ hipError_t launch_forward_128(const Params& p, int shape, int64_t items, int64_t
                               hipStream_t stream) {
   if (shape == kWide) return launch_attn<128, kWide>(p, items, merges, n_hg, stream);
   if (shape == kLong) return launch_attn<128, kLong>(p, items, merges, n_hg, stream);
+  if (shape == kDual) return launch_attn<128, kDual>(p, items, merges, n_hg, stream);
   return hipErrorInvalidValue;
 }
 #endif  // KA_FWD_UNIT

@@ -32,19 +32,29 @@
 
 namespace karpo {
 
-enum TileShape : int { kWide = 0, kNarrow = 1, kSmall = 2, kLong = 3 };
+enum TileShape : int { kWide = 0, kNarrow = 1, kSmall = 2, kLong = 3, kDual = 4 };
+
+// Head size 128 prefill in dual-block tiles (kDual): eight waves, two per SIMD, each holding two 32-vector query
+// blocks, so every K / V operand read from LDS feeds two MFMAs and each wave has two independent softmaxes to
+// interleave with its products. Built as a variant when KA_DUAL is 0 (the twelve-wave tile then serves those runs).
+#ifndef KA_DUAL
+#define KA_DUAL 1
+#endif
 
 // Waves per workgroup (each holds 32 query vectors of the tile, a pair of waves at head_dim 512), keys per step and
 // workgroups resident per CU (the register and LDS budget of the kernel), per head size and tile shape.
 KA_HD constexpr int tile_waves(int head_dim, int shape) {
   return shape == kNarrow ? (head_dim == 512 ? 2 : 1)
          : shape == kSmall ? 4
+         : shape == kDual ? 8
          : head_dim == 512 ? 8 : head_dim == 128 ? 12 : head_dim == 256 ? 8 : 4;
 }
-// Query vectors per tile: 32 per wave, or per pair of waves at head_dim 512 (each wave of a pair holds half of every
-// vector's elements: half of Q's operands and of O's accumulators).
+// 32-vector query blocks per wave (per pair of waves at head_dim 512): two in the dual-block tiles, else one.
+KA_HD constexpr int tile_blocks(int head_dim, int shape) { return shape == kDual ? 2 : 1; }
+// Query vectors per tile: 32 per block of a wave, or of a pair of waves at head_dim 512 (each wave of a pair holds
+// half of every vector's elements: half of Q's operands and of O's accumulators).
 KA_HD constexpr int tile_vectors(int head_dim, int shape) {
-  return 32 * tile_waves(head_dim, shape) / (head_dim == 512 ? 2 : 1);
+  return 32 * tile_waves(head_dim, shape) * tile_blocks(head_dim, shape) / (head_dim == 512 ? 2 : 1);
 }
 KA_HD constexpr int tile_keys(int head_dim, int shape) {
   return head_dim == 64 ? 64 : head_dim >= 256 ? 32 : shape == kLong ? 64 : 32;
@@ -103,6 +113,7 @@ KA_HD inline int tile_shape(int heads, int kv_heads, int head_dim, int64_t max_q
     if (gather || (head_dim == 128 && max_q <= 4096) || (head_dim == 256 && max_q <= 8192)) return kSmall;
   }
   if (head_dim == 128 && max_q > 65536) return kLong;
+  if (head_dim == 128 && KA_DUAL) return kDual;
   return kWide;
 }
 KA_HD inline Geometry geometry(int heads, int kv_heads, int head_dim, int64_t max_q, bool gather = false) {

@@ -27,6 +27,12 @@ KA_HD inline void v_dma_source(int blk, int lane, int* key, int* col) {
   *col = (b % (D / 16)) * 16 + (piece & 1) * 8;
 }
 
+// The tile vector that lane column `col` (0-31) of wave `wave` holds in its query block `block`: a wave's blocks (a
+// pair's, at head_dim 512, where both waves hold the same vectors) are consecutive 32-vector runs of the tile.
+KA_HD inline int lane_vector(int wave, int block, int col, bool pair, int blocks) {
+  return ((pair ? wave >> 1 : wave) * blocks + block) * 32 + col;
+}
+
 // The keys query `pos` of a sequence sees (qa: the sequence's first query row in the pack, lq / lk: its query and key
 // rows, query i at key coordinate i + lk - lq): [lo, hi) from the (left, right) window (-1: unbounded), and [sl, sh)
 // from the image span holding its row (spans: sorted, non-overlapping half-open query-row ranges), empty when none.

@@ -93,21 +93,43 @@ def test_every_gradient_row_is_written(gpu, name):
     assert all(layer["written"].values()), layer["written"]
 
 
+@functools.lru_cache(maxsize=None)
+def _oracle(name: str, g: int, dtype: torch.dtype):
+    layer = _layer(name)
+    q_cu, k_cu, scale, left, right, spans, _ = layer["w"]
+    q, k, v, do = layer["groups"][g]["inputs"]
+    print(f"layer {name}: oracle ({dtype}) for key/value head {g}", flush=True)
+    return oa.packed_grads(q, k, v, do, q_cu, k_cu, scale, left, right, spans, dtype=dtype)
+
+
+def _group(name: str, which: str) -> int:
+    return 0 if which == "first" else _layer(name)["w"][-1] - 1
+
+
 @pytest.mark.parametrize("which", ["first", "last"])
 @pytest.mark.parametrize("name", LAYERS)
 def test_head_group_gradients_match_the_oracle(gpu, name, which):
-    """The first or last key/value head group's out, dq, dk, dv against autograd through the oracle (float32), and
-    against twice the oracle's own bf16 error plus 2e-3."""
-    layer = _layer(name)
-    q_cu, k_cu, scale, left, right, spans, kv_heads = layer["w"]
-    g = 0 if which == "first" else kv_heads - 1
-    q, k, v, do = layer["groups"][g]["inputs"]
-    got = layer["groups"][g]["got"]
-    print(f"layer {name}: oracle for key/value head {g}", flush=True)
-    want = oa.packed_grads(q, k, v, do, q_cu, k_cu, scale, left, right, spans, dtype=torch.float32)
-    base = oa.packed_grads(q, k, v, do, q_cu, k_cu, scale, left, right, spans, dtype=torch.bfloat16)
+    """The first or last key/value head group's out, dq, dk, dv against autograd through the oracle in float32:
+    relative Frobenius error below 1e-2."""
+    g = _group(name, which)
+    got = _layer(name)["groups"][g]["got"]
+    want = _oracle(name, g, torch.float32)
+    for label, x, w in zip(("out", "dq", "dk", "dv"), got, want):
+        r = rel(x, w)
+        print(name, g, label, f"rel {r:.2e}", flush=True)
+        assert r < REL_FRO, (label, r)
+
+
+@pytest.mark.parametrize("which", ["first", "last"])
+@pytest.mark.parametrize("name", LAYERS)
+def test_head_group_gradients_within_twice_the_bf16_error(gpu, name, which):
+    """The same gradients within twice the error of the oracle's own bf16 run plus 2e-3 (both against the float32
+    oracle): the reference's criterion for its backward kernels."""
+    g = _group(name, which)
+    got = _layer(name)["groups"][g]["got"]
+    want = _oracle(name, g, torch.float32)
+    base = _oracle(name, g, torch.bfloat16)
     for label, x, w, b in zip(("out", "dq", "dk", "dv"), got, want, base):
         r, rb = rel(x, w), rel(b, w)
         print(name, g, label, f"rel {r:.2e} (oracle bf16 {rb:.2e})", flush=True)
-        assert r < REL_FRO, (label, r)
         assert r < 2 * rb + 2e-3, (label, r, rb)

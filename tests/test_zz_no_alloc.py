@@ -1,11 +1,17 @@
 """karpo_attn_fwd_noalloc (the forward with its scratch in the library's own device array) against karpo_attn_fwd
 with a caller's workspace, through the C ABI: two calls in a row, the second on a smaller input, each bitwise equal to
 the workspace call. The packs split tiles over their keys (the partials live in the scratch), plan on the device
-and from a host plan, and read keys through a row table."""
+and from a host plan, and read keys through a row table. Under HIP graph capture (the callers it is for): the first
+call on the device made inside a capture, in a process of its own (tests/noalloc_capture.py), replayed with rewritten
+bounds."""
 
 from __future__ import annotations
 
 import ctypes
+import json
+import subprocess
+import sys
+from pathlib import Path
 
 import pytest
 import torch
@@ -97,3 +103,20 @@ def test_noalloc_decode_shaped_and_row_table_calls(gpu):
     want = _call("workspace", q2, k, v, cu2, cu2, 600, 0.088, -1, 0, rows=rows)
     got = _call("noalloc", q2, k, v, cu2, cu2, 600, 0.088, -1, 0, rows=rows)
     assert torch.equal(got, want)
+
+
+def test_noalloc_first_call_inside_a_graph_capture(gpu):
+    """The entry point's first call on the device made inside a capture (a fresh process, tests/noalloc_capture.py):
+    the call succeeds, every replay with rewritten bounds equals the workspace entry point's eager call bit for bit
+    and writes every row, and eager calls after the first leave the device's free memory unchanged."""
+    child = Path(__file__).resolve().parent / "noalloc_capture.py"
+    done = subprocess.run([sys.executable, "-u", str(child)], capture_output=True, text=True, timeout=180)
+    print(done.stdout[-3000:], done.stderr[-3000:], flush=True)
+    assert done.returncode == 0, done.stderr[-3000:]
+    result = json.loads(done.stdout.strip().splitlines()[-1])
+    assert result["status_in_capture"] == 0, result
+    assert len(result["replays"]) == 5
+    for r in result["replays"]:
+        assert r["equal"] and not r["nan"], r
+    assert result["eager_status"] == [0, 0, 0]
+    assert len(set(result["free_bytes"])) == 1, result["free_bytes"]
