@@ -38,7 +38,7 @@ enum TileShape : int { kWide = 0, kNarrow = 1, kSmall = 2, kLong = 3, kDual = 4 
 // blocks, so every K / V operand read from LDS feeds two MFMAs and each wave has two independent softmaxes to
 // interleave with its products. Built as a variant when KA_DUAL is 0 (the twelve-wave tile then serves those runs).
 #ifndef KA_DUAL
-#define KA_DUAL 1
+#define KA_DUAL 0
 #endif
 
 // Waves per workgroup (each holds 32 query vectors of the tile, a pair of waves at head_dim 512), keys per step and
