@@ -243,13 +243,14 @@ int karpo_attn_device_status(const KarpoAttnArgs* args, void* stream, int32_t* s
 int karpo_attn_plan(const KarpoAttnArgs* args, const int32_t* q_cu_host, const int32_t* k_cu_host, int32_t n_seq,
                     int32_t* plan, int64_t capacity);
 
-/* Query rows per tile, keys per step and query heads per work item the kernel uses for these heads / head size, the
- * longest query run max_q and row-table use (gather nonzero: the call sets k_rows): packs whose sequences fit one
- * wave's 32 query vectors take one-wave tiles; runs up to 4,096 queries at head size 128 (8,192 at 256), and every
- * run read through a row table at those head sizes, take 4-wave tiles; longer ones the wide tiles (12 waves at 128,
- * 32 keys per step; 64 keys per step above 65,536 queries). */
+/* Query rows per tile, keys per step, query heads per work item and the tile shape (plan header entry 10: 0 wide,
+ * 1 one-wave, 2 four-wave, 3 long, 4 dual-block) the kernel uses for these heads / head size, the longest query run
+ * max_q and row-table use (gather nonzero: the call sets k_rows): packs whose sequences fit one wave's 32 query
+ * vectors take one-wave tiles; runs up to 4,096 queries at head size 128 (8,192 at 256), and every run read through a
+ * row table at those head sizes, take 4-wave tiles; longer ones the prefill tiles (at 128: 32 keys per step, 64 above
+ * 65,536 queries). Any output pointer may be NULL. */
 int karpo_attn_tile_shape(int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t max_q, int32_t gather,
-                          int32_t* rows_per_tile, int32_t* keys_per_step, int32_t* heads_per_item);
+                          int32_t* rows_per_tile, int32_t* keys_per_step, int32_t* heads_per_item, int32_t* shape);
 
 /* A static message for a status code. */
 const char* karpo_attn_strerror(int status);

@@ -100,7 +100,7 @@ def load() -> ctypes.CDLL:
         lib.karpo_attn_workspace_bytes.restype = ctypes.c_int
         lib.karpo_attn_tile_shape.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                                               ctypes.c_int32, P(ctypes.c_int32), P(ctypes.c_int32),
-                                              P(ctypes.c_int32)]
+                                              P(ctypes.c_int32), P(ctypes.c_int32)]
         lib.karpo_attn_tile_shape.restype = ctypes.c_int
         lib.karpo_attn_strerror.argtypes = [ctypes.c_int]
         lib.karpo_attn_strerror.restype = ctypes.c_char_p
@@ -136,20 +136,15 @@ def check(status: int, what: str) -> None:
 LONG = 1 << 30
 
 
+@functools.lru_cache(maxsize=1024)
 def kernel_shape(heads: int, kv_heads: int, head_dim: int, max_q: int = LONG, gather: bool = False) -> int:
     """The forward kernel's tile-shape template argument for these heads, longest query run and row-table use (0
     wide, 1 narrow: one wave, or one pair at head_dim 512; 2 small: four waves at head_dim 128 / 256; 3 long: 64-key
-    steps at 128), as read off tile_shape's geometry."""
-    rows, keys, per = tile_shape(heads, kv_heads, head_dim, max_q, gather)
-    vectors = rows * per
-    waves = vectors // 32 * (2 if head_dim == 512 else 1)
-    if vectors == 32:
-        return 1
-    if head_dim in (128, 256) and waves == 4:
-        return 2
-    if head_dim == 128 and keys == 64:
-        return 3
-    return 0
+    steps at 128; 4 dual-block: two query blocks per wave at 128)."""
+    shape = ctypes.c_int32()
+    check(load().karpo_attn_tile_shape(heads, kv_heads, head_dim, max_q, int(bool(gather)), None, None, None,
+                                       ctypes.byref(shape)), "karpo_attn_tile_shape")
+    return shape.value
 
 
 @functools.lru_cache(maxsize=1024)
@@ -160,5 +155,5 @@ def tile_shape(heads: int, kv_heads: int, head_dim: int, max_q: int = LONG,
     function of its arguments, asked on every planned call)."""
     rows, keys, per = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
     check(load().karpo_attn_tile_shape(heads, kv_heads, head_dim, max_q, int(bool(gather)), ctypes.byref(rows),
-                                       ctypes.byref(keys), ctypes.byref(per)), "karpo_attn_tile_shape")
+                                       ctypes.byref(keys), ctypes.byref(per), None), "karpo_attn_tile_shape")
     return rows.value, keys.value, per.value

@@ -1454,7 +1454,7 @@ hipError_t launch_forward(const Params& p, int head_dim, const Geometry& g, int6
     case 128 * 8 + kNarrow: return launch_attn<128, kNarrow>(p, items, merges, g.n_hg, stream);
     case 128 * 8 + kSmall: return launch_attn<128, kSmall>(p, items, merges, g.n_hg, stream);
     case 128 * 8 + kLong: return launch_forward_128(p, kLong, items, merges, g.n_hg, stream);
-    case 128 * 8 + kDual: return launch_forward_128(p, kDual, items, merges, g.n_hg, stream);
+    case 128 * 8 + kDual: return launch_attn<128, kDual>(p, items, merges, g.n_hg, stream);
     case 256 * 8 + kWide: return launch_attn<256, kWide>(p, items, merges, g.n_hg, stream);
     case 256 * 8 + kNarrow: return launch_attn<256, kNarrow>(p, items, merges, g.n_hg, stream);
     case 256 * 8 + kSmall: return launch_attn<256, kSmall>(p, items, merges, g.n_hg, stream);
@@ -1475,7 +1475,6 @@ hipError_t launch_forward_128(const Params& p, int shape, int64_t items, int64_t
                               hipStream_t stream) {
   if (shape == kWide) return launch_attn<128, kWide>(p, items, merges, n_hg, stream);
   if (shape == kLong) return launch_attn<128, kLong>(p, items, merges, n_hg, stream);
-  if (shape == kDual) return launch_attn<128, kDual>(p, items, merges, n_hg, stream);
   return hipErrorInvalidValue;
 }
 #endif  // KA_FWD_UNIT

@@ -122,7 +122,7 @@ extern "C" const char* karpo_attn_strerror(int status) {
 
 extern "C" int karpo_attn_tile_shape(int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t max_q,
                                      int32_t gather, int32_t* rows_per_tile, int32_t* keys_per_step,
-                                     int32_t* heads_per_item) {
+                                     int32_t* heads_per_item, int32_t* shape) {
   if (heads < 1 || kv_heads < 1 || heads % kv_heads != 0) return KARPO_ATTN_ERR_HEADS;
   if (!head_dim_supported(head_dim)) return KARPO_ATTN_ERR_HEAD_DIM;
   if (max_q < 0) return KARPO_ATTN_ERR_ARG;
@@ -130,6 +130,7 @@ extern "C" int karpo_attn_tile_shape(int32_t heads, int32_t kv_heads, int32_t he
   if (rows_per_tile) *rows_per_tile = g.rows;
   if (keys_per_step) *keys_per_step = g.bn;
   if (heads_per_item) *heads_per_item = g.ng;
+  if (shape) *shape = g.shape;
   return KARPO_ATTN_OK;
 }
 

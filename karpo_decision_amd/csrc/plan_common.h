@@ -36,9 +36,10 @@ enum TileShape : int { kWide = 0, kNarrow = 1, kSmall = 2, kLong = 3, kDual = 4 
 
 // Head size 128 prefill in dual-block tiles (kDual): eight waves, two per SIMD, each holding two 32-vector query
 // blocks, so every K / V operand read from LDS feeds two MFMAs and each wave has two independent softmaxes to
-// interleave with its products. Built as a variant when KA_DUAL is 0 (the twelve-wave tile then serves those runs).
+// interleave with its products (7.08 against 7.44 ms for the twelve-wave tile at the 32k layer, bitwise equal
+// outputs). KA_DUAL 0 builds the twelve-wave tile for those runs instead (for A/B measurements).
 #ifndef KA_DUAL
-#define KA_DUAL 0
+#define KA_DUAL 1
 #endif
 
 // Waves per workgroup (each holds 32 query vectors of the tile, a pair of waves at head_dim 512), keys per step and
@@ -113,7 +114,10 @@ KA_HD inline int tile_shape(int heads, int kv_heads, int head_dim, int64_t max_q
     if (gather || (head_dim == 128 && max_q <= 4096) || (head_dim == 256 && max_q <= 8192)) return kSmall;
   }
   if (head_dim == 128 && max_q > 65536) return kLong;
-  if (head_dim == 128 && KA_DUAL) return kDual;
+  // dual-block tiles (512 vectors) unless the GQA group divides the twelve-wave tile's 384 vectors but not 512 (3, 6,
+  // 12, ...): the twelve-wave tile then stages one K/V stream for the whole group, the dual tile one per head
+  const int group = heads / kv_heads;
+  if (head_dim == 128 && KA_DUAL && !(384 % group == 0 && 512 % group != 0)) return kDual;
   return kWide;
 }
 KA_HD inline Geometry geometry(int heads, int kv_heads, int head_dim, int64_t max_q, bool gather = false) {

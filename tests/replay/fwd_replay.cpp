@@ -59,7 +59,7 @@ int replay(const Call& c, Report& r, std::vector<uint8_t>& written) {
   const Geometry g = c.force_shape >= 0 ? geometry_of(a->heads, a->kv_heads, D, c.force_shape)
                                          : geometry(a->heads, a->kv_heads, D, a->max_q, gather);
   const FwdSizes z = fwd_sizes(a->total_q, a->n_seq, a->max_q, D, g);
-  const int W = g.waves, BN = g.bn;
+  const int W = g.waves, BN = g.bn, QB = tile_blocks(D, g.shape);
   const bool pair = D == 512;
   const int NB = kv_buffers(D, g.shape, gather);
   const int TILE = BN * D * 2, BLKS = TILE / 1024, INSTS = (BLKS + W - 1) / W;
@@ -109,8 +109,9 @@ int replay(const Call& c, Report& r, std::vector<uint8_t>& written) {
     // the lanes' keys and the workgroup's envelope
     int klo = INT32_MAX, khi = INT32_MIN;
     for (int w = 0; w < W; ++w)
+      for (int b = 0; b < QB; ++b)
       for (int col = 0; col < 32; ++col) {
-        const int vec = (pair ? (w >> 1) : w) * 32 + col;
+        const int vec = lane_vector(w, b, col, pair, QB);
         const int off = vec / g.ng, pos = tile * g.rows + off, head = hg * g.ng + (vec - off * g.ng);
         if (pos >= lq) continue;
         const LaneKeys k = lane_keys(pos, qa, lq, lk, a->window_left, a->window_right, c.spans, a->n_spans);
@@ -229,9 +230,10 @@ int replay(const Call& c, Report& r, std::vector<uint8_t>& written) {
     }
     // the store: the tile's rows, or this part's partial
     for (int w = 0; w < W; ++w)
+      for (int b = 0; b < QB; ++b)
       for (int lane = 0; lane < 64; ++lane) {
         const int col = lane & 31, half = lane >> 5;
-        const int vec = (pair ? (w >> 1) : w) * 32 + col;
+        const int vec = lane_vector(w, b, col, pair, QB);
         const int off = vec / g.ng, pos = tile * g.rows + off, head = hg * g.ng + (vec - off * g.ng);
         const int dh = pair ? (w & 1) : 0;
         if (parts > 1) {

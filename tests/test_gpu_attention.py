@@ -209,13 +209,16 @@ def test_branched_varlen_with_an_empty_sequence(gpu, heads, kv_heads, head, caus
     assert_close(got, want, f"branched causal={causal}")
 
 
-@pytest.mark.parametrize("heads,kv_heads,head,shapes", [(32, 16, 128, {1400: 2, 5000: 0, 70000: 3}),
+@pytest.mark.parametrize("heads,kv_heads,head,shapes", [(32, 16, 128, {1400: 2, 5000: 4, 70000: 3}),
                                                        (12, 4, 128, {1400: 2, 5000: 0, 70000: 3}),
+                                                       (10, 2, 128, {1400: 2, 5000: 4, 70000: 3}),
                                                        (16, 8, 256, {1400: 2, 9000: 0})])
 @pytest.mark.parametrize("left", [-1, 200])
 def test_every_tile_shape_matches_the_oracle(gpu, heads, kv_heads, head, shapes, left):
-    """max_q is an upper bound of the query runs that selects the tile shape (small, wide, long; the narrow shape has
-    its own tests): one pack run under each shape its max_q values select, each against the oracle."""
+    """max_q is an upper bound of the query runs that selects the tile shape (small, dual-block, wide, long; the
+    narrow shape has its own tests; a GQA group of 3 takes the twelve-wave wide tile at head size 128, one of 5 the
+    dual-block tile with one head per item): one pack run under each shape its max_q values select, each against
+    the oracle."""
     torch.manual_seed(5)
     lengths = [1400, 513, 1, 700]
     cu = _lengths_cu(lengths)
@@ -400,8 +403,8 @@ def _plan_parts(plan: torch.Tensor) -> tuple[list[int], list[tuple], list[tuple]
 def test_every_row_is_written_and_device_plan_matches_host_plan(gpu):
     """Through the C ABI: an output pre-filled with NaN has no NaN left; the device planner's work list is the host
     planner's (same header and split tiles, the same items as a multiset, ordered by non-increasing cost); running
-    from the host plan gives the same bits. The Qwen-class pack in the wide tile shape (max_q 8192: above the small
-    shape's runs) is small enough that its longest tiles split."""
+    from the host plan gives the same bits. The Qwen-class pack in the dual-block tile shape (max_q 8192: above the
+    small shape's runs) is small enough that its longest tiles split."""
     w = workloads.qwen_full(gpu, seed=7)
     q_cu = torch.tensor(w.q_cu, dtype=torch.int32, device=gpu)
     max_q = 8192
@@ -409,7 +412,7 @@ def test_every_row_is_written_and_device_plan_matches_host_plan(gpu):
     ws = _c_abi_call(w.query, w.key, w.value, o, q_cu, q_cu, max_q, w.scale, -1, 0)
     assert not torch.isnan(o).any()
     plan = ops.make_plan(w.q_cu, w.k_cu, w.heads, w.kv_heads, w.head_dim, -1, 0, device=gpu, max_q=max_q)
-    assert plan.header[5] == 12
+    assert plan.header[5] == 8 and plan.header[10] == 4  # eight waves of two query blocks
     host_header, host_merges, host_items = _plan_parts(plan.tensor)
     dev_header, dev_merges, dev_items = _plan_parts(ws.view(torch.int32)[: plan.tensor.numel()])
     assert host_header[4] > 0, "expected split tiles in this pack"
@@ -431,7 +434,8 @@ def test_every_row_is_written_and_device_plan_matches_host_plan(gpu):
 
 
 @pytest.mark.parametrize("heads,kv_heads,head,max_q,decode,shape", [
-    (8, 2, 128, 6000, False, 0), (8, 2, 128, 4096, False, 2), (8, 2, 128, 70000, False, 3), (8, 2, 128, 1, True, 1),
+    (8, 2, 128, 6000, False, 4), (12, 4, 128, 6000, False, 0), (8, 2, 128, 4096, False, 2),
+    (8, 2, 128, 70000, False, 3), (8, 2, 128, 1, True, 1),
     (8, 2, 64, 6000, False, 0), (8, 2, 64, 1, True, 1), (8, 2, 256, 9000, False, 0), (8, 2, 256, 4096, False, 2),
     (8, 2, 256, 1, True, 1), (8, 2, 512, 6000, False, 0), (8, 2, 512, 1, True, 1)])
 def test_split_tiles_device_plan_matches_host_plan(gpu, heads, kv_heads, head, max_q, decode, shape):

@@ -70,9 +70,10 @@ GEOMETRIES = [(8, 2, 64), (16, 8, 128), (32, 16, 128), (16, 8, 256), (12, 4, 128
               (32, 4, 512), (6, 2, 512)]
 
 
-def waves_of(rows, per, head_dim):
-    """Waves of a tile: 32 query vectors per wave, per pair of waves at head_dim 512."""
-    return rows * per // 32 * (2 if head_dim == 512 else 1)
+def waves_of(rows, per, head_dim, shape=0):
+    """Waves of a tile: 32 query vectors per wave (64 in the dual-block tiles, shape 4), per pair of waves at
+    head_dim 512."""
+    return rows * per // (64 if shape == 4 else 32) * (2 if head_dim == 512 else 1)
 
 
 def expected_plan(q_cu, k_cu, heads, kv_heads, head_dim, left, right, max_q):
@@ -101,7 +102,8 @@ def test_host_plan_matches_brute_force(q_lens, extra, geom, left, right, short):
     max_q = max(q_lens)
     rows, bn, per, narrow, merges, items = expected_plan(q_cu, k_cu, heads, kv_heads, head_dim, left, right, max_q)
     header, got_merges, got_items = host_plan(q_cu, k_cu, heads, kv_heads, head_dim, left, right, max_q)
-    assert header[:7] == [len(items), rows, bn, per, len(merges), waves_of(rows, per, head_dim),
+    shape = _lib.kernel_shape(heads, kv_heads, head_dim, max_q)
+    assert header[:7] == [len(items), rows, bn, per, len(merges), waves_of(rows, per, head_dim, shape),
                           _lib.PLAN_HEADER + 4 * len(merges)]
     assert header[7] == sum(m[2] for m in merges)
     assert header[8:] == [len(q_cu) - 1, 0, _lib.kernel_shape(heads, kv_heads, head_dim, max_q), 0]
@@ -141,17 +143,20 @@ def test_markers_plan_splits_keys():
 def test_tile_geometry():
     # a tile holds 32 query vectors per wave (12 waves at head_dim 128, 8 at 256, 4 at 64); the GQA group's heads
     # share it when they divide it. Head size 128: 32-key steps, 64 for runs above 65,536 queries
-    assert _lib.tile_shape(32, 16, 128, 32768) == (192, 32, 2)
-    assert _lib.tile_shape(32, 16, 128, 65536) == (192, 32, 2)
+    # head size 128 prefill: dual-block tiles of 512 vectors (eight waves of two 32-vector blocks), 32-key steps
+    assert _lib.tile_shape(32, 16, 128, 32768) == (256, 32, 2)
+    assert _lib.tile_shape(32, 16, 128, 65536) == (256, 32, 2)
     assert _lib.tile_shape(32, 16, 128, 65537) == (192, 64, 2)
     assert _lib.tile_shape(32, 16, 128) == (192, 64, 2)
     assert _lib.tile_shape(8, 2, 64) == (32, 64, 4)
     assert _lib.tile_shape(16, 8, 256) == (128, 32, 2)
     assert _lib.tile_shape(12, 4, 128) == (128, 64, 3)  # a group of 3 divides 384 vectors
+    assert _lib.tile_shape(12, 4, 128, 5000) == (128, 32, 3)  # and not 512: the twelve-wave tile shares K/V
     assert _lib.tile_shape(10, 2, 128) == (384, 64, 1)  # a group of 5 does not: one head per item
+    assert _lib.tile_shape(10, 2, 128, 5000) == (512, 32, 1)
     # small tiles (4 waves) for runs up to 4,096 queries at head size 128 and 8,192 at 256
     assert _lib.tile_shape(32, 16, 128, 4096) == (64, 32, 2)
-    assert _lib.tile_shape(32, 16, 128, 4097) == (192, 32, 2)
+    assert _lib.tile_shape(32, 16, 128, 4097) == (256, 32, 2)
     assert _lib.tile_shape(16, 8, 256, 8192) == (64, 32, 2)
     assert _lib.tile_shape(16, 8, 256, 8193) == (128, 32, 2)
     assert _lib.tile_shape(12, 4, 128, 1000) == (128, 32, 1)  # a group of 3 does not divide 128 vectors
@@ -168,7 +173,8 @@ def test_tile_geometry():
     assert _lib.tile_shape(32, 4, 512, 4) == (4, 32, 8)
     assert _lib.tile_shape(6, 2, 512) == (128, 32, 1)  # a group of 3 does not divide 128 vectors
     # the kernels' shape numbering (wide 0, narrow 1, small 2, long 3), as bench.py labels the launch
-    assert [_lib.kernel_shape(32, 16, 128, n) for n in (32768, 16, 4096, 65537)] == [0, 1, 2, 3]
+    assert [_lib.kernel_shape(32, 16, 128, n) for n in (32768, 16, 4096, 65537)] == [4, 1, 2, 3]
+    assert _lib.kernel_shape(12, 4, 128, 32768) == 0  # the twelve-wave tile for a group of 3
     assert [_lib.kernel_shape(16, 8, 256, n) for n in (16384, 8192)] == [0, 2]
     assert [_lib.kernel_shape(32, 4, 512, n) for n in (32768, 4)] == [0, 1]
 

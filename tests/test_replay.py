@@ -19,7 +19,7 @@ from karpo_decision_amd import _lib, ops, workloads
 
 ROOT = Path(__file__).resolve().parents[1]
 SOURCE = ROOT / "tests" / "replay" / "fwd_replay.cpp"
-WIDE, NARROW, SMALL, LONG = 0, 1, 2, 3
+WIDE, NARROW, SMALL, LONG, DUAL = 0, 1, 2, 3, 4
 
 
 @pytest.fixture(scope="module")
@@ -100,10 +100,10 @@ def test_branched_pack_under_the_tile_that_faulted(replay):
     assert past == 0
 
 
-@pytest.mark.parametrize("shape,max_q", [(WIDE, 5000), (LONG, 70000), (SMALL, 4096)])
+@pytest.mark.parametrize("shape,max_q", [(DUAL, 5000), (LONG, 70000), (SMALL, 4096)])
 def test_branched_row_tables_under_every_head_128_shape(replay, shape, max_q):
     """Branches of uneven lengths (partial key steps, so table rows past a sequence read at the resource's end)
-    under the wide, long and four-wave tiles at head size 128."""
+    under the dual-block, long and four-wave tiles at head size 128."""
     q_cu, k_cu, rows = _branched(prompts=2, shared=1000, branches=3, branch=37)
     bad, counts, first = run_replay(replay, q_cu, k_cu, 32, 16, 128, -1, 0, rows=rows, max_q=max_q,
                                     plan_max_q=max_q, plan_gather=shape == SMALL, force_shape=shape,
