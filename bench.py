@@ -325,12 +325,20 @@ def main() -> int:
     value = flops / (ms_per_step * 1e-3) / 1e12
     achieved = flops / (launch_ms * 1e-3) / 1e12
 
-    traffic = None
+    shape = _lib.kernel_shape(w.heads, w.kv_heads, w.head_dim, w.max_q, gather)
+    # the head-size-512 prefill tile without a row table runs as the pair ping-pong kernel
+    kernel = ("attn_fwd_pair_pp_kernel" if (w.head_dim, shape, gather) == (512, 0, False)
+              else f"attn_fwd_kernel<{w.head_dim}, {shape}, {str(gather).lower()}>")
+    # HBM traffic per launch is not counted in this run (it needs rocprofv3 counter passes, see profiles/): it is the
+    # recorded figure for this workload's kernel, with where and when it was recorded, or null when none matches
+    traffic, traffic_source = None, None
     if TRAFFIC.exists():
         entry = json.loads(TRAFFIC.read_text()).get(w.name)
-        if entry:
+        if entry and entry.get("kernel") == kernel:
             traffic = entry.get("bytes_per_launch")
-    shape = _lib.kernel_shape(w.heads, w.kv_heads, w.head_dim, w.max_q, gather)
+            traffic_source = (f"not measured in this run: {TRAFFIC.relative_to(ROOT)}, rocprofv3 FETCH_SIZE x "
+                              f"{entry.get('fetch_factor')} + WRITE_SIZE x {entry.get('write_factor')} per dispatch of "
+                              f"{entry.get('kernel')} ({entry.get('summary')}, recorded {entry.get('recorded', '?')})")
     if w.bound(PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)) == "mfma":
         roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_BF16_TFLOPS, 4)}
@@ -347,8 +355,7 @@ def main() -> int:
                    "pct_of_bf16_peak": round(100 * value / PEAK_BF16_TFLOPS, 2),
                    "tokens_per_s": round(w.tokens / (ms_per_step * 1e-3)), "flops_per_step": flops,
                    "min_hbm_bytes_per_step": w.bytes(), "parallelism": "single GPU"},
-        "roofline": {**roof, "traffic": traffic,
-                     "kernel": f"attn_fwd_kernel<{w.head_dim}, {shape}, {str(gather).lower()}>",
+        "roofline": {**roof, "traffic": traffic, "traffic_source": traffic_source, "kernel": kernel,
                      "avg_launch_ms": round(launch_ms, 4)},
     }
     if not args.no_cpu_baseline:

@@ -56,6 +56,9 @@ namespace karpo {
 // one 8-wave workgroup per CU, 64 KiB LDS; D=512 one 8-wave workgroup (four pairs, two waves per SIMD), 128 KiB LDS.
 // Small: 4-wave workgroups, three per CU at D=128 (32 KiB LDS each), two at D=256 (64 KiB). Narrow: one wave per
 // workgroup (a pair at D=512), 32 KiB LDS (64 KiB at D=256, 128 KiB at D=512), LDS-limited to five (two, one) per CU.
+// s_barrier without the fence __syncthreads adds (which waits for every outstanding copy)
+__device__ __forceinline__ void bare_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
 template <int D, int SHAPE> struct TileCfg {
   static constexpr int W = tile_waves(D, SHAPE);
   static constexpr int BN = tile_keys(D, SHAPE);
@@ -551,19 +554,8 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
   wait_next(-1);
   __syncthreads();
 
-  // step s: copy step s + NB - 1 into (kn, vn) while computing on (kt, vt); then wait for step s + 1's copy
-  auto step = [&](int s, const KA_LDS char* kt, const KA_LDS char* vt, KA_LDS char* kn, KA_LDS char* vn) {
-    const int j0 = j_first + s * BN;
-    if (s + NB - 1 < n_steps) copy_step(j0 + (NB - 1) * BN, kn, vn);
-    if (GATHER && s + NB < n_steps) fetch_rows(j0 + NB * BN);
-    const bool active = j0 < whi && j0 + BN > wlo;  // wave-uniform: some query of this wave sees a key of the step
-    if (PAIR || active) {  // a pair enters together (its barriers), each wave computes only when active
-    f32x16 st[QB][KB];
-#pragma unroll
-    for (int b = 0; b < QB; ++b)
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb) st[b][kb] = f32x16{};
-    if (active) {
+  // S^T of a step's keys (st zeroed by the caller), K from the tile kt
+  auto qk_products = [&](const KA_LDS char* kt, f32x16 (&st)[QB][KB]) {
 #pragma unroll
       for (int dc = 0; dc < QC; ++dc) {
 #pragma unroll
@@ -574,31 +566,9 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
             st[b][kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qop[b][dc], st[b][kb], 0, 0, 0);
         }
       }
-    }
-    if constexpr (PAIR) {
-      // the pair adds its two partial S^T through LDS: each wave's 16 floats per lane go to its 4 KiB exchange slot
-      // (read by the partner after the barrier; written again only after the step's end barrier)
-      static_assert(KB == 1, "one 32-key block per step");
-      KA_LDS f32x4* slot = (KA_LDS f32x4*)&xch[wave][0] + lane;
-      const KA_LDS f32x4* other = (const KA_LDS f32x4*)&xch[wave ^ 1][0] + lane;
-      if (active) {
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4)
-          slot[q4 * 64] = f32x4{st[0][0][4 * q4], st[0][0][4 * q4 + 1], st[0][0][4 * q4 + 2], st[0][0][4 * q4 + 3]};
-      }
-      __syncthreads();
-      if (active) {
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {  // a sum of two terms: equal in both waves (addition commutes exactly)
-          const f32x4 o = other[q4 * 64];
-          st[0][0][4 * q4] += o.x;
-          st[0][0][4 * q4 + 1] += o.y;
-          st[0][0][4 * q4 + 2] += o.z;
-          st[0][0][4 * q4 + 3] += o.w;
-        }
-      }
-    }
-    if (active) {
+  };
+  // the step's masks, softmax and P.V products (V from the tile vt) on its S^T
+  auto softmax_pv = [&](int j0, const KA_LDS char* vt, f32x16 (&st)[QB][KB]) {
       bf16x8 pb[QB][KC];
 #pragma unroll
       for (int b = 0; b < QB; ++b) {
@@ -665,7 +635,45 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
             acc[b][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[b][kc], acc[b][db], 0, 0, 0);
         }
       }
+  };
+
+  // step s: copy step s + NB - 1 into (kn, vn) while computing on (kt, vt); then wait for step s + 1's copy
+  auto step = [&](int s, const KA_LDS char* kt, const KA_LDS char* vt, KA_LDS char* kn, KA_LDS char* vn) {
+    const int j0 = j_first + s * BN;
+    if (s + NB - 1 < n_steps) copy_step(j0 + (NB - 1) * BN, kn, vn);
+    if (GATHER && s + NB < n_steps) fetch_rows(j0 + NB * BN);
+    const bool active = j0 < whi && j0 + BN > wlo;  // wave-uniform: some query of this wave sees a key of the step
+    if (PAIR || active) {  // a pair enters together (its barriers), each wave computes only when active
+    f32x16 st[QB][KB];
+#pragma unroll
+    for (int b = 0; b < QB; ++b)
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) st[b][kb] = f32x16{};
+    if (active) qk_products(kt, st);
+    if constexpr (PAIR) {
+      // the pair adds its two partial S^T through LDS: each wave's 16 floats per lane go to its 4 KiB exchange slot
+      // (read by the partner after the barrier; written again only after the step's end barrier)
+      static_assert(KB == 1, "one 32-key block per step");
+      KA_LDS f32x4* slot = (KA_LDS f32x4*)&xch[wave][0] + lane;
+      const KA_LDS f32x4* other = (const KA_LDS f32x4*)&xch[wave ^ 1][0] + lane;
+      if (active) {
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4)
+          slot[q4 * 64] = f32x4{st[0][0][4 * q4], st[0][0][4 * q4 + 1], st[0][0][4 * q4 + 2], st[0][0][4 * q4 + 3]};
+      }
+      __syncthreads();
+      if (active) {
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {  // a sum of two terms: equal in both waves (addition commutes exactly)
+          const f32x4 o = other[q4 * 64];
+          st[0][0][4 * q4] += o.x;
+          st[0][0][4 * q4 + 1] += o.y;
+          st[0][0][4 * q4 + 2] += o.z;
+          st[0][0][4 * q4 + 3] += o.w;
+        }
+      }
     }
+    if (active) softmax_pv(j0, vt, st);
     }
     wait_next(s);
     __syncthreads();
@@ -752,8 +760,6 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
 // its own LDS work and copies explicitly), so the copies stay in flight across the middle barrier. The arithmetic is
 // attn_fwd_kernel's but for the order in which l adds up a step's 16 P values (two partial sums).
 
-// s_barrier without the fence __syncthreads adds (which waits for every outstanding copy)
-__device__ __forceinline__ void bare_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 __global__ __launch_bounds__(512, 2) void attn_fwd_pair_pp_kernel(Params p) {
   constexpr int D = 512, W = 8, BN = 32;
