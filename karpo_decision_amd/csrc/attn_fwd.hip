@@ -59,6 +59,14 @@ namespace karpo {
 // s_barrier without the fence __syncthreads adds (which waits for every outstanding copy)
 __device__ __forceinline__ void bare_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
+// The maximum of 16 scores as a tree of depth three (v_max3 nodes): the serial chain would be eight deep.
+__device__ __forceinline__ float max16(const f32x16& v) {
+  const float t0 = fmaxf(fmaxf(v[0], v[1]), v[2]), t1 = fmaxf(fmaxf(v[3], v[4]), v[5]);
+  const float t2 = fmaxf(fmaxf(v[6], v[7]), v[8]), t3 = fmaxf(fmaxf(v[9], v[10]), v[11]);
+  const float t4 = fmaxf(fmaxf(v[12], v[13]), v[14]);
+  return fmaxf(fmaxf(fmaxf(t0, t1), t2), fmaxf(fmaxf(t3, t4), v[15]));
+}
+
 template <int D, int SHAPE> struct TileCfg {
   static constexpr int W = tile_waves(D, SHAPE);
   static constexpr int BN = tile_keys(D, SHAPE);
@@ -570,9 +578,9 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
   // the step's masks, softmax and P.V products (V from the tile vt) on its S^T
   auto softmax_pv = [&](int j0, const KA_LDS char* vt, f32x16 (&st)[QB][KB]) {
       bf16x8 pb[QB][KC];
+      if (!(j0 >= wflo && j0 + BN <= wfhi)) {  // some query of this wave does not see every key of the step
 #pragma unroll
-      for (int b = 0; b < QB; ++b) {
-        if (!(j0 >= wflo && j0 + BN <= wfhi)) {  // some query of this wave does not see every key of the step
+        for (int b = 0; b < QB; ++b) {
           int klo_ = lo[b], khi_ = hi[b], ksl = sl[b], ksh = sh[b];
           if constexpr (KEYS_IN_LDS) {
             const int4 kk = keys_lds[b * W * 64 + tid];
@@ -591,21 +599,43 @@ __global__ __launch_bounds__((64 * TileCfg<D, SHAPE>::W), (TileCfg<D, SHAPE>::OC
               st[b][kb][jj] = vis ? st[b][kb][jj] : -INFINITY;
             }
         }
+      }
+      // each block's row maximum (with two blocks a tree of depth three per 16 scores, the blocks side by side: 32k
+      // layer 7.06 -> 6.94 ms; the one-block tiles keep the chain, which measured as fast or faster there), then one
+      // uniform branch for the rare steps where some block raises its running maximum
+      float mt[QB];
+      bool need[QB], any = false;
+#pragma unroll
+      for (int b = 0; b < QB; ++b) {
         float mx = -INFINITY;
+        if constexpr (QB > 1) {
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb)
+          for (int kb = 0; kb < KB; ++kb) mx = fmaxf(mx, max16(st[b][kb]));
+        } else {
 #pragma unroll
-          for (int jj = 0; jj < 16; ++jj) mx = fmaxf(mx, st[b][kb][jj]);
-        const float mt = half_swap_max(mx) * c;
-        const bool need = mt > m[b] + p.tau;
-        if (__builtin_amdgcn_ballot_w64(need)) {  // raise the running maximum (rare after the first steps)
-          const float mn = need ? mt : m[b];
-          const float alpha = need ? __builtin_amdgcn_exp2f(m[b] - mn) : 1.f;  // from the start value: alpha = 0
-          m[b] = mn;
-          l[b] *= alpha;
+          for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-          for (int db = 0; db < OB; ++db) acc[b][db] *= alpha;
+            for (int jj = 0; jj < 16; ++jj) mx = fmaxf(mx, st[b][kb][jj]);
         }
+        mt[b] = half_swap_max(mx) * c;
+        need[b] = mt[b] > m[b] + p.tau;
+        any |= need[b];
+      }
+      if (QB == 1 || __builtin_amdgcn_ballot_w64(any)) {
+#pragma unroll
+        for (int b = 0; b < QB; ++b) {
+          if (__builtin_amdgcn_ballot_w64(need[b])) {  // raise the running maximum (rare after the first steps)
+            const float mn = need[b] ? mt[b] : m[b];
+            const float alpha = need[b] ? __builtin_amdgcn_exp2f(m[b] - mn) : 1.f;  // from the start value: 0
+            m[b] = mn;
+            l[b] *= alpha;
+#pragma unroll
+            for (int db = 0; db < OB; ++db) acc[b][db] *= alpha;
+          }
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < QB; ++b) {
 #pragma unroll
         for (int kc = 0; kc < KC; ++kc) {
 #pragma unroll
