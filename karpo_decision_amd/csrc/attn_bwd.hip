@@ -17,10 +17,11 @@
 //     the query rows that see the tile streamed in steps of 32 rows of one head (every head of the GQA group in turn,
 //     which sums the group's gradients): S = Q K^T and dP = dO V^T with Q and dO as row operands, dV^T += dO^T P and
 //     dK^T += Q^T dS with Q and dO read transposed from the same tiles (S layout; a dV-only launch stages dO in the
-//     transposed-read layout, whose copies read whole rows). One launch computes both (MODE 3; at head size 256 one
-//     wave per SIMD holds both accumulators in 256 AGPRs), or, at head size 128 for packs with many key tiles, two
-//     launches compute dV (MODE 1) and dK (MODE 2), each recomputing S (two or three waves per SIMD instead of one
-//     overlap each other's softmax and MFMA work; a small pack has too few tiles to fill the GPU twice).
+//     transposed-read layout, whose copies read whole rows). One launch computes both (MODE 3; at head sizes 64 and
+//     256 one wave per SIMD holds both accumulators in 256 AGPRs);
+//   * bwd_dkdv2_kernel (head size 128): both gradients in one launch at two waves per SIMD, eight waves per key tile
+//     in two groups that take alternate row steps, K and V in LDS instead of registers (30.7 -> 28.1 ms for the 32k
+//     layer's backward against dV and dK as two launches, MODE 1 and MODE 2, each recomputing S: KA_BWD2 0).
 // Both streams advance their copy addresses by pointer increments per step (no per-step address recomputation: the
 // scalar unit is shared by the CU's waves and a step is short).
 // Rows of a product's row operand are fed in the order that swaps bits 2 and 3 of the row index (key_row), so each
@@ -41,6 +42,11 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 // Key-tile workgroups from which head size 128 runs dK and dV as two launches.
 constexpr int64_t kSplitKeyTiles = 8 * kComputeUnits;
+// Head size 128 computes dK and dV in bwd_dkdv2_kernel; KA_BWD2 0 restores the two launches (large packs) or the
+// one-wave-per-SIMD MODE 3 launch (small packs), for A/B measurements.
+#ifndef KA_BWD2
+#define KA_BWD2 1
+#endif
 
 template <int D> struct BwdCfg {
   static constexpr int OCC_Q = D >= 256 ? 1 : 2;  // waves per SIMD the registers are budgeted for
@@ -641,6 +647,350 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::template occ_k<MODE>()) 
   }
 }
 
+// ---- dK and dV in one launch with two waves per SIMD (head size 128): eight waves per key tile of 128 keys, as two
+// groups of four (group rs = wave / 4, each wave of a group holding 32 keys) that take alternate query-row steps of
+// the tile's rows (group 0 steps 0, 2, .., group 1 steps 1, 3, ..). K and V of the tile sit in LDS (the S layout,
+// read as the B operands of S = Q K^T and dP = dO V^T) instead of registers, which leaves room for both fp32
+// accumulators at 256 registers; at the end group 1's sums are added to group 0's through LDS in a fixed order
+// (repeated calls stay bitwise equal). Four products per step instead of the five of the dV and dK launches.
+template <int D>
+__global__ __launch_bounds__(64 * 2 * kBwdWaves, 2) void bwd_dkdv2_kernel(BwdParams p) {
+  constexpr int KW = kBwdWaves, W = 2 * KW, BQ = kBwdStep;
+  constexpr int KT = 32 * KW;  // keys per tile
+  constexpr int DC = D / 16, DB = D / 32, KC = BQ / 16;
+  constexpr int TILE = BQ * D * 2, BLKS = TILE / 1024, INSTS = BLKS / KW;  // a step's copies per wave of a group
+  constexpr int KTILE = KT * D * 2, KINSTS = KTILE / 1024 / W;              // the K (and V) tile's per wave
+  static_assert(BLKS % KW == 0 && (KTILE / 1024) % W == 0, "every wave issues the same copies");
+  static_assert(2 * KTILE >= 2 * KW * 32 * D * 4 / 2, "the tiles hold one accumulator of group 1 at a time");
+  __shared__ __attribute__((aligned(1024))) char kt_lds[KTILE];  // K of the tile's keys (S layout)
+  __shared__ __attribute__((aligned(1024))) char vt_lds[KTILE];  // V of the tile's keys (S layout)
+  __shared__ __attribute__((aligned(1024))) char qk0[2][TILE];   // per group: Q (S layout), two buffers
+  __shared__ __attribute__((aligned(1024))) char qk1[2][TILE];
+  __shared__ __attribute__((aligned(1024))) char ok0[2][TILE];   // per group: dO (S layout)
+  __shared__ __attribute__((aligned(1024))) char ok1[2][TILE];
+  __shared__ __attribute__((aligned(256))) float sts0[2][2 * BQ];  // per group: log2 LSE, then D, of the step's rows
+  __shared__ __attribute__((aligned(256))) float sts1[2][2 * BQ];
+  __shared__ int red[2][KW];
+
+  if (p.plan[2] != BQ || p.plan[5] != KW) return;
+  const int item = blockIdx.x / p.n_hg;
+  const int kvh = blockIdx.x - item * p.n_hg;
+  if (item >= p.plan[0]) return;
+  const int32_t* entry = p.plan + p.plan[6] + kItemInts * item;
+  const int seg = entry[0], ktile = entry[1];
+  const int part = entry[2] & 0xffff, parts = entry[2] >> 16;
+  const int slot = entry[3];
+  if (parts > 1 && (slot < 0 || slot + part >= p.slots)) return;  // a partial slot outside the workspace
+  const int keys_per_tile = p.plan[1];
+  const int qa = p.q_cu[seg], lq = p.q_cu[seg + 1] - qa;
+  const int ka = p.k_cu[seg], lk = p.k_cu[seg + 1] - ka;
+  const int delta = lk - lq;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kw = wave & (KW - 1), rs = wave / KW;
+  const int col = lane & 31, half = lane >> 5;
+
+  // this lane's key and the query rows that see it (as bwd_dkdv_kernel)
+  const int key = ktile * keys_per_tile + kw * 32 + col;
+  const bool valid = key < lk;
+  int rlo = 0, rhi = 0, srl = 0, srh = 0;
+  int wlo = INT32_MAX, whi = INT32_MIN, wflo = INT32_MIN, wfhi = INT32_MAX;
+  if (valid) {
+    int a = p.right < 0 ? 0 : max(0, key - p.right - delta);
+    int b = p.left < 0 ? lq : (int)min((int64_t)lq, (int64_t)key + p.left - delta + 1);
+    if (b < a) b = a;
+    rlo = a;
+    rhi = b;
+    wflo = a;
+    wfhi = b;
+    if (a < b) {
+      wlo = a;
+      whi = b;
+    }
+    const int kq = key - delta;
+    if (p.n_spans > 0 && kq >= 0 && kq < lq) {
+      const int row = qa + kq;
+      int l0 = 0, l1 = p.n_spans;
+      while (l1 - l0 > 1) {
+        const int mid = (l0 + l1) >> 1;
+        if (p.spans[2 * mid] <= row) l0 = mid; else l1 = mid;
+      }
+      const int s0 = p.spans[2 * l0], s1 = p.spans[2 * l0 + 1];
+      if (s0 <= row && row < s1) {
+        const int x = max(0, s0 - qa), y = min(lq, s1 - qa);
+        if (x < y) {
+          srl = x;
+          srh = y;
+          wlo = min(wlo, x);
+          whi = max(whi, y);
+        }
+      }
+    }
+  }
+  wlo = __builtin_amdgcn_readfirstlane(wave_min(wlo));
+  whi = __builtin_amdgcn_readfirstlane(wave_max(whi));
+  wflo = __builtin_amdgcn_readfirstlane(wave_max(wflo));
+  wfhi = __builtin_amdgcn_readfirstlane(wave_min(wfhi));
+  if (lane == 0 && rs == 0) {  // group 1 holds the same keys
+    red[0][kw] = wlo;
+    red[1][kw] = whi;
+  }
+  // K and V of the tile's keys into LDS (keys past the sequence read as zeros)
+  {
+    const int rows = min(lk - ktile * keys_per_tile, KT);
+    const uint16_t* kb = p.k + (int64_t)(ka + ktile * keys_per_tile) * p.sk_t + (int64_t)kvh * p.sk_h;
+    const uint16_t* vb = p.v + (int64_t)(ka + ktile * keys_per_tile) * p.sv_t + (int64_t)kvh * p.sv_h;
+#pragma unroll
+    for (int r = 0; r < KINSTS; ++r) {
+      int row, colm;
+      s_dma_source<D>(wave * KINSTS + r, lane, &row, &colm);
+      dma_16b(kb, rows * (int)p.sk_t * 2, (KA_LDS char*)kt_lds + (wave * KINSTS + r) * 1024,
+              (uint32_t)(row * p.sk_t + colm) * 2u);
+      dma_16b(vb, rows * (int)p.sv_t * 2, (KA_LDS char*)vt_lds + (wave * KINSTS + r) * 1024,
+              (uint32_t)(row * p.sv_t + colm) * 2u);
+    }
+  }
+  __syncthreads();
+  int qlo = INT32_MAX, qhi = INT32_MIN;
+#pragma unroll
+  for (int w = 0; w < KW; ++w) {
+    qlo = min(qlo, red[0][w]);
+    qhi = max(qhi, red[1][w]);
+  }
+  qlo = __builtin_amdgcn_readfirstlane(qlo);
+  qhi = __builtin_amdgcn_readfirstlane(qhi);
+  const int r_first = qlo < qhi ? (qlo / BQ) * BQ : 0;
+  const int n_rsteps = qlo < qhi ? (qhi - r_first + BQ - 1) / BQ : 0;
+  const int all_steps = n_rsteps * p.group;
+  const int s_begin = parts > 1 ? (int)((int64_t)part * all_steps / parts) : 0;
+  const int n_steps = parts > 1 ? (int)((int64_t)(part + 1) * all_steps / parts) - s_begin : all_steps;
+  const int my_steps = n_steps > rs ? (n_steps - rs + 1) / 2 : 0;  // this group's: s_begin + rs + 2 i
+  const int n_iter = (n_steps + 1) / 2;
+
+  const int gofs = rs * TILE;  // this group's buffers in the two-group arrays
+  uint32_t qk_off[INSTS], ok_off[INSTS];
+#pragma unroll
+  for (int r = 0; r < INSTS; ++r) {
+    int row, colm;
+    s_dma_source<D>(kw * INSTS + r, lane, &row, &colm);
+    qk_off[r] = (uint32_t)(row * p.sq_t + colm) * 2u;
+    ok_off[r] = (uint32_t)(row * p.sdo_t + colm) * 2u;
+  }
+  // the steps in bwd_dkdv_kernel's order (rows downwards, then the group's next head), each group taking every other
+  const int r_last = r_first + (n_rsteps - 1) * BQ;
+  const int h0 = kvh * p.group;
+  const int64_t q_step = (int64_t)BQ * p.sq_t, o_step = (int64_t)BQ * p.sdo_t;
+  const int64_t q_wrap = p.sq_h + n_rsteps * q_step, o_wrap = p.sdo_h + n_rsteps * o_step;
+  const int64_t st_wrap = 2 * p.total_q + (int64_t)n_rsteps * BQ;
+  const int h_begin = n_rsteps > 0 ? s_begin / n_rsteps : 0;
+  const int r_begin = r_last - (s_begin - h_begin * n_rsteps) * BQ;
+  int c_r0 = r_begin;
+  const uint16_t* c_q = p.q + (int64_t)(qa + r_begin) * p.sq_t + (int64_t)(h0 + h_begin) * p.sq_h;
+  const uint16_t* c_o = p.dout + (int64_t)(qa + r_begin) * p.sdo_t + (int64_t)(h0 + h_begin) * p.sdo_h;
+  const float* c_st = p.stats + (int64_t)(h0 + h_begin) * 2 * p.total_q + qa + r_begin;
+  auto advance = [&]() {
+    c_r0 -= BQ;
+    c_q -= q_step;
+    c_o -= o_step;
+    c_st -= BQ;
+    if (c_r0 < r_first) {  // the group's next head
+      c_r0 = r_last;
+      c_q += q_wrap;
+      c_o += o_wrap;
+      c_st += st_wrap;
+    }
+  };
+  auto next_row = [&](int r) { return r == r_first ? r_last : r - BQ; };
+  int r_cur = r_begin;
+  if (rs == 1 && n_steps > 1) {
+    advance();
+    r_cur = next_row(r_cur);
+  }
+  auto copy_step = [&](KA_LDS char* tqk, KA_LDS char* tok, KA_LDS float* tst) {
+    const int rows = min(lq - c_r0, BQ);
+    const uint16_t* qs = c_q;
+    const uint16_t* os = c_o;
+    const float* src = c_st;
+    advance();
+    advance();
+#pragma unroll
+    for (int r = 0; r < INSTS; ++r) {
+      const int at = gofs + (kw * INSTS + r) * 1024;
+      dma_16b(qs, rows * (int)p.sq_t * 2, tqk + at, qk_off[r]);
+      dma_16b(os, rows * (int)p.sdo_t * 2, tok + at, ok_off[r]);
+    }
+    if (kw == KW - 1) {  // 32 log2 LSE (lanes 0-31) then 32 D (lanes 32-63), 4 B per lane; zeros past the stats
+      const __amdgpu_buffer_rsrc_t rsrc =
+          __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, (int)(p.total_q + rows) * 4, kBufferFlags);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (KA_LDS void*)(tst + 2 * BQ * rs), 4,
+                                               (uint32_t)((lane >> 5) * p.total_q + (lane & 31)) * 4u, 0, 0, 0);
+    }
+  };
+  // the group's buffers are [rs] of the two-group arrays: its offset rides in the lanes' read offsets, so the
+  // buffers' bases stay constants (a per-group base register left the reads' constant offsets unfolded: spills)
+  const int q_read[2] = {gofs + s_offset<D>(key_row(col), half), gofs + s_offset<D>(key_row(col), 2 + half)};
+  const int k_read[2] = {s_offset<D>(kw * 32 + col, half), s_offset<D>(kw * 32 + col, 2 + half)};
+  const int t_read[2] = {gofs + s_tr_base(lane, 0), gofs + s_tr_base(lane, 1)};
+  f32x16 dk[DB], dv[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+    dk[db] = f32x16{};
+    dv[db] = f32x16{};
+  }
+  const float c = p.c;
+  const KA_LDS char* const kt = (const KA_LDS char*)kt_lds;
+  const KA_LDS char* const vt = (const KA_LDS char*)vt_lds;
+  KA_LDS char* const tqk0 = (KA_LDS char*)qk0;
+  KA_LDS char* const tqk1 = (KA_LDS char*)qk1;
+  KA_LDS char* const tok0 = (KA_LDS char*)ok0;
+  KA_LDS char* const tok1 = (KA_LDS char*)ok1;
+  KA_LDS float* const tst0 = (KA_LDS float*)sts0;
+  KA_LDS float* const tst1 = (KA_LDS float*)sts1;
+  if (my_steps > 0) copy_step(tqk0, tok0, tst0);
+  wait_vmcnt<0>();
+  __syncthreads();
+
+  auto step = [&](int i, const KA_LDS char* tqk, const KA_LDS char* tok, const KA_LDS float* tst, KA_LDS char* nqk,
+                  KA_LDS char* nok, KA_LDS float* nst) {
+    if (i + 1 < my_steps) copy_step(nqk, nok, nst);
+    const int r0 = r_cur;
+    r_cur = next_row(next_row(r_cur));
+    if (i < my_steps && r0 < whi && r0 + BQ > wlo) {
+      // the lanes' read offsets, opaque per step: their sums with the reads' constants stay in the instructions'
+      // offset fields instead of 16 registers held across the loop
+      int qr0 = q_read[0], qr1 = q_read[1], kr0 = k_read[0], kr1 = k_read[1], tr0 = t_read[0], tr1 = t_read[1];
+      asm volatile("" : "+v"(qr0), "+v"(qr1), "+v"(kr0), "+v"(kr1), "+v"(tr0), "+v"(tr1));
+      const int qr[2] = {qr0, qr1}, kr[2] = {kr0, kr1}, tr[2] = {tr0, tr1};
+      f32x16 st = f32x16{}, dpt = f32x16{};
+#pragma unroll
+      for (int dc = 0; dc < DC; ++dc) {
+        const int at = (dc >> 1) * 1024;
+        const bf16x8 a = *(const KA_LDS bf16x8*)(tqk + qr[dc & 1] + at);
+        const bf16x8 kb = *(const KA_LDS bf16x8*)(kt + kr[dc & 1] + at);
+        st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, kb, st, 0, 0, 0);
+        const bf16x8 b = *(const KA_LDS bf16x8*)(tok + qr[dc & 1] + at);
+        const bf16x8 vb = *(const KA_LDS bf16x8*)(vt + kr[dc & 1] + at);
+        dpt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, vb, dpt, 0, 0, 0);
+      }
+      f32x4 ls[4], ds[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int r = 2 * BQ * rs + (u >> 1) * 16 + half * 8 + (u & 1) * 4;
+        ls[u] = *(const KA_LDS f32x4*)(tst + r);
+        ds[u] = *(const KA_LDS f32x4*)(tst + BQ + r);
+      }
+      float x[2 * KC * 4];
+#pragma unroll
+      for (int jj = 0; jj < 2 * KC * 4; ++jj) x[jj] = __builtin_fmaf(st[jj], c, -ls[jj >> 2][jj & 3]);
+      if (!(r0 >= wflo && r0 + BQ <= wfhi)) {
+#pragma unroll
+        for (int jj = 0; jj < 2 * KC * 4; ++jj) {
+          const int row = r0 + result_row(jj, half);
+          const bool vis =
+              ((unsigned)(row - rlo) < (unsigned)(rhi - rlo)) | ((unsigned)(row - srl) < (unsigned)(srh - srl));
+          x[jj] = vis ? x[jj] : -INFINITY;
+        }
+      }
+      bf16x8 pb[KC], dsb[KC];
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          const int jj = kc * 8 + t;
+          const float pr = __builtin_amdgcn_exp2f(x[jj]);
+          pb[kc][t] = (__bf16)pr;
+          dsb[kc][t] = (__bf16)(pr * (dpt[jj] - ds[jj >> 2][jj & 3]));
+        }
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) {
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          bf16x4 ov[2], qv[2];
+#pragma unroll
+          for (int rr = 0; rr < 2; ++rr) {
+            const int at = tr[rr] + kc * (D / 8) * 256 + db * 1024;
+            ov[rr] = __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((KA_LDS s16x4*)(tok + at)));
+            qv[rr] = __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((KA_LDS s16x4*)(tqk + at)));
+          }
+          const bf16x8 ao = __builtin_shufflevector(ov[0], ov[1], 0, 1, 2, 3, 4, 5, 6, 7);
+          dv[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ao, pb[kc], dv[db], 0, 0, 0);
+          const bf16x8 aq = __builtin_shufflevector(qv[0], qv[1], 0, 1, 2, 3, 4, 5, 6, 7);
+          dk[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aq, dsb[kc], dk[db], 0, 0, 0);
+        }
+      }
+    }
+    wait_vmcnt<0>();
+    __syncthreads();
+  };
+  int i = 0;
+  for (; i + 1 < n_iter; i += 2) {
+    step(i, tqk0, tok0, tst0, tqk1, tok1, tst1);
+    step(i + 1, tqk1, tok1, tst1, tqk0, tok0, tst0);
+  }
+  if (i < n_iter) step(i, tqk0, tok0, tst0, tqk1, tok1, tst1);
+
+  // group 1's sums to group 0 through the K and V tiles (no longer read): dK, then dV, 16 KiB per wave
+  KA_LDS f32x4* const xs = (KA_LDS f32x4*)((kw < 2 ? (KA_LDS char*)kt_lds : (KA_LDS char*)vt_lds) + (kw & 1) * 16384) +
+                           lane;
+#pragma unroll
+  for (int which = 0; which < 2; ++which) {
+    f32x16(&acc)[DB] = which == 0 ? dk : dv;
+    if (rs == 1) {
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4)
+          xs[(db * 4 + g4) * 64] = f32x4{acc[db][g4 * 4], acc[db][g4 * 4 + 1], acc[db][g4 * 4 + 2], acc[db][g4 * 4 + 3]};
+    }
+    __syncthreads();
+    if (rs == 0) {
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const f32x4 y = xs[(db * 4 + g4) * 64];
+          acc[db][g4 * 4] += y.x;
+          acc[db][g4 * 4 + 1] += y.y;
+          acc[db][g4 * 4 + 2] += y.z;
+          acc[db][g4 * 4 + 3] += y.w;
+        }
+    }
+    __syncthreads();
+  }
+  if (rs == 1) return;
+
+  if (parts > 1) {  // one part of a split tile: fp32 dK (before the scale) and dV for bwd_merge_kernel
+    float* base = p.partial + bwd_partial_base(slot, part, p.n_hg, kvh, KT, D) + (kw * 32 + col) * D + half * 4;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        *(float4*)(base + db * 32 + g4 * 8) = float4{dk[db][g4 * 4], dk[db][g4 * 4 + 1], dk[db][g4 * 4 + 2],
+                                                     dk[db][g4 * 4 + 3]};
+        *(float4*)(base + KT * D + db * 32 + g4 * 8) = float4{dv[db][g4 * 4], dv[db][g4 * 4 + 1],
+                                                              dv[db][g4 * 4 + 2], dv[db][g4 * 4 + 3]};
+      }
+    return;
+  }
+  if (valid) {  // lane (col, half) holds d = db*32 + (j/4)*8 + half*4 + j%4 of its key
+    uint16_t* kq = p.dk + (int64_t)(ka + key) * p.sdk_t + (int64_t)kvh * p.sdk_h + half * 4;
+    uint16_t* vq = p.dv + (int64_t)(ka + key) * p.sdv_t + (int64_t)kvh * p.sdv_h + half * 4;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        u32x2 a;
+        a[0] = pack_bf16(dk[db][g4 * 4] * p.scale, dk[db][g4 * 4 + 1] * p.scale);
+        a[1] = pack_bf16(dk[db][g4 * 4 + 2] * p.scale, dk[db][g4 * 4 + 3] * p.scale);
+        *(u32x2*)(kq + db * 32 + g4 * 8) = a;
+        u32x2 b;
+        b[0] = pack_bf16(dv[db][g4 * 4], dv[db][g4 * 4 + 1]);
+        b[1] = pack_bf16(dv[db][g4 * 4 + 2], dv[db][g4 * 4 + 3]);
+        *(u32x2*)(vq + db * 32 + g4 * 8) = b;
+      }
+  }
+}
+
 // ---- the split key tiles' merge: dK = scale * sum_p dK_p, dV = sum_p dV_p, summed in part order. Thread per (split
 // tile, key/value head, key, dK or dV, 4 elements of D), in a grid-stride loop over a fixed grid.
 constexpr int kBwdMergeThreads = 256;
@@ -710,7 +1060,9 @@ static hipError_t launch_bwd_d(const BwdParams& p, const Geometry& gq, const Geo
   pk.n_hg = gk.n_hg;
   const dim3 grid((unsigned)(items_k * gk.n_hg));
   if (items_k > 0) {
-    if (D == 128 && tiles_k * gk.n_hg >= kSplitKeyTiles) {
+    if (D == 128 && KA_BWD2) {
+      if constexpr (D == 128) hipLaunchKernelGGL(bwd_dkdv2_kernel<D>, grid, dim3(2 * 64 * kBwdWaves), 0, stream, pk);
+    } else if (D == 128 && tiles_k * gk.n_hg >= kSplitKeyTiles) {
       if constexpr (D == 128) {
         hipLaunchKernelGGL((bwd_dkdv_kernel<D, 1>), grid, dim3(64 * kBwdWaves), 0, stream, pk);
         hipLaunchKernelGGL((bwd_dkdv_kernel<D, 2>), grid, dim3(64 * kBwdWaves), 0, stream, pk);

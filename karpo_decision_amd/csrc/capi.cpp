@@ -391,10 +391,12 @@ extern "C" int karpo_attn_bwd(const KarpoAttnBwdArgs* b, void* stream) {
                              b->d_k_stride_tok,  b->d_k_stride_head,  b->d_v_stride_tok,  b->d_v_stride_head};
   for (int64_t s : strides)
     if (!check_stride(s)) return KARPO_ATTN_ERR_LAYOUT;
-  // a step's rows (32 keys, or 32 query rows) are addressed with 32-bit byte offsets
+  // a step's rows (32 keys, or 32 query rows) and a key tile's (the 128 keys the dK / dV kernel stages) are
+  // addressed with 32-bit byte offsets
   const int64_t d = a->head_dim;
-  if ((a->k_stride_tok + d) * bwd_q_step(a->head_dim) * 2 >= (int64_t)INT32_MAX ||
-      (a->v_stride_tok + d) * bwd_q_step(a->head_dim) * 2 >= (int64_t)INT32_MAX ||
+  const int64_t key_rows = 32 * kBwdWaves > bwd_q_step(a->head_dim) ? 32 * kBwdWaves : bwd_q_step(a->head_dim);
+  if ((a->k_stride_tok + d) * key_rows * 2 >= (int64_t)INT32_MAX ||
+      (a->v_stride_tok + d) * key_rows * 2 >= (int64_t)INT32_MAX ||
       (a->q_stride_tok + d) * kBwdStep * 2 >= (int64_t)INT32_MAX ||
       (b->d_o_stride_tok + d) * kBwdStep * 2 >= (int64_t)INT32_MAX || (a->total_q + kBwdStep) * 4 >= INT32_MAX)
     return KARPO_ATTN_ERR_LAYOUT;
