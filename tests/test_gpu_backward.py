@@ -177,7 +177,7 @@ def test_long_key_tiles_split_over_their_query_steps(gpu, monkeypatch, q_lens):
     steps (each part of the dK / dV kernel stores fp32 partials, bwd_merge_kernel sums them in part order). The key
     tiles' plan in the workspace (which starts as garbage) lists split tiles; the gradients match the oracle and
     repeated calls are bitwise equal. With 260 one-token sequences beside it the key tiles number 2,296 workgroups of
-    capacity (8 key/value heads), so dK and dV run as two launches, each storing its own half of the partials."""
+    capacity (8 key/value heads); each part's two row-step groups add their sums before the part stores them."""
     seen = []
     real = ops._workspace
 
@@ -227,9 +227,9 @@ def test_backward_refuses_what_it_does_not_take(gpu):
         ops.packed_attention_backward(out, q, q, q, out, lse[:, :4], cu, cu, 8, 0.1, -1, 0, None)
 
 
-def test_many_key_tiles_take_the_two_launch_path(gpu):
-    """Head size 128 with 32 key/value heads over 8,192 keys: enough key tiles for dK and dV to run as two launches
-    (each recomputing P), against the oracle like the one-launch packs above."""
+def test_many_key_tiles(gpu):
+    """Head size 128 with 32 key/value heads over 8,192 keys (2,048 key-tile workgroups, eight GPU-fulls), against
+    the oracle like the smaller packs above."""
     q, k, v, do, q_cu, k_cu, spans = make_pack([6000, 2192], [6000, 2192], 32, 32, 128, seed=31)
     got = kernel_grads(q, k, v, do, q_cu, k_cu, 128 ** -0.5, -1, 0, spans)
     want = oa.packed_grads(q, k, v, do, q_cu, k_cu, 128 ** -0.5, -1, 0, spans, dtype=torch.float32)

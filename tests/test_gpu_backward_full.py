@@ -2,7 +2,7 @@
 
 Four layers, each run whole through the C ABI (the forward's output and log-sum-exp from ``packed_attention_lse``,
 then ``karpo_attn_bwd`` into NaN-filled dQ, dK and dV): the 32k-token global layer (32 / 16 heads, head_dim 128,
-causal; its dK / dV run as two launches), the 16k sliding layer (16 / 8 heads, head_dim 256, window 1023), the Qwen
+causal; its dK / dV in the two-group kernel), the 16k sliding layer (16 / 8 heads, head_dim 256, window 1023), the Qwen
 8k pack (16 / 8 heads, head_dim 128, causal) and the 31B global layer (32 / 4 heads, head_dim 512, causal, the pair
 kernels). Checks:
 
