@@ -171,7 +171,8 @@ def test_backward_is_deterministic(gpu):
         assert torch.equal(x, y)
 
 
-@pytest.mark.parametrize("q_lens", [[2000, 100, 37], [3000] + [1] * 260], ids=["one-launch", "two-launch"])
+@pytest.mark.parametrize("q_lens", [[2000, 100, 37], [3000] + [1] * 260],
+                         ids=["mixed-lengths", "many-short-sequences"])
 def test_long_key_tiles_split_over_their_query_steps(gpu, monkeypatch, q_lens):
     """One long causal sequence among short ones: the device planner splits its first key tiles over their query
     steps (each part of the dK / dV kernel stores fp32 partials, bwd_merge_kernel sums them in part order). The key
