@@ -661,7 +661,7 @@ __global__ __launch_bounds__(64 * 2 * kBwdWaves, 2) void bwd_dkdv2_kernel(BwdPar
   constexpr int TILE = BQ * D * 2, BLKS = TILE / 1024, INSTS = BLKS / KW;  // a step's copies per wave of a group
   constexpr int KTILE = KT * D * 2, KINSTS = KTILE / 1024 / W;              // the K (and V) tile's per wave
   static_assert(BLKS % KW == 0 && (KTILE / 1024) % W == 0, "every wave issues the same copies");
-  static_assert(2 * KTILE >= 2 * KW * 32 * D * 4 / 2, "the tiles hold one accumulator of group 1 at a time");
+  static_assert(2 * KTILE >= KW * 32 * D * 4, "the K and V tiles hold group 1's fp32 dK (or dV) at the end");
   __shared__ __attribute__((aligned(1024))) char kt_lds[KTILE];  // K of the tile's keys (S layout)
   __shared__ __attribute__((aligned(1024))) char vt_lds[KTILE];  // V of the tile's keys (S layout)
   __shared__ __attribute__((aligned(1024))) char qk0[2][TILE];   // per group: Q (S layout), two buffers
