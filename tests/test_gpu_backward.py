@@ -65,6 +65,8 @@ LAYOUTS = [
     ([200], [200], 8, 8, 128, -1, 0, [(0, 30, 90), (0, 120, 121)], None),  # image spans under causal
     ([160, 33], [160, 33], 4, 2, 128, 5, 7, [(0, 40, 72)], None),       # two-sided window and a span
     ([129, 77], [129, 77], 6, 2, 128, -1, 0, [], None),                  # group 3 does not divide a tile
+    ([700, 333], [700, 333], 16, 2, 128, -1, 0, [], None),               # group 8: steps cross head boundaries
+    ([500, 47], [500, 47], 16, 4, 128, 100, 0, [], None),                # group 4 under a window
     ([100], [130], 4, 2, 128, 31, 0, [], -0.09),                         # negative scale, window, branch
     ([96, 64], [96, 64], 4, 2, 256, -1, 0, [(1, 8, 40)], None),
     ([300, 1, 0, 130], [300, 1, 0, 130], 8, 1, 512, -1, 0, [], None),   # head size 512: wave pairs
