@@ -335,6 +335,55 @@ __global__ __launch_bounds__(64 * bwd_q_waves(D), BwdCfg<D>::BLOCKS_Q) void bwd_
   }
 }
 
+// The query rows that see key `key` of a sequence (qa: the sequence's first query row in the pack; lq, delta = lk -
+// lq): rows [lo, hi) by the window (j - right <= i + delta <= j + left) and [sl, sh), the image span holding the
+// key's aligned row, when it is in one; and over the wave, the envelope [wlo, whi) of the rows any lane's key is seen
+// by and the range [wflo, wfhi) of rows that see every lane's key. A lane past the sequence (not valid) sees none.
+struct KeyRows {
+  int lo, hi, sl, sh;
+  int wlo, whi, wflo, wfhi;
+};
+__device__ __forceinline__ KeyRows key_rows_seen(const BwdParams& p, int key, bool valid, int qa, int lq, int delta) {
+  KeyRows r = {0, 0, 0, 0, INT32_MAX, INT32_MIN, INT32_MIN, INT32_MAX};
+  if (valid) {
+    int a = p.right < 0 ? 0 : max(0, key - p.right - delta);
+    int b = p.left < 0 ? lq : (int)min((int64_t)lq, (int64_t)key + p.left - delta + 1);
+    if (b < a) b = a;
+    r.lo = a;
+    r.hi = b;
+    r.wflo = a;
+    r.wfhi = b;
+    if (a < b) {
+      r.wlo = a;
+      r.whi = b;
+    }
+    const int kq = key - delta;  // the key's position in query rows
+    if (p.n_spans > 0 && kq >= 0 && kq < lq) {
+      const int row = qa + kq;
+      int l0 = 0, l1 = p.n_spans;
+      while (l1 - l0 > 1) {
+        const int mid = (l0 + l1) >> 1;
+        if (p.spans[2 * mid] <= row) l0 = mid; else l1 = mid;
+      }
+      const int s0 = p.spans[2 * l0], s1 = p.spans[2 * l0 + 1];
+      if (s0 <= row && row < s1) {
+        const int x = max(0, s0 - qa), y = min(lq, s1 - qa);
+        if (x < y) {
+          r.sl = x;
+          r.sh = y;
+          r.wlo = min(r.wlo, x);
+          r.whi = max(r.whi, y);
+        }
+      }
+    }
+  }
+  r.wlo = __builtin_amdgcn_readfirstlane(wave_min(r.wlo));
+  r.whi = __builtin_amdgcn_readfirstlane(wave_max(r.whi));
+  r.wflo = __builtin_amdgcn_readfirstlane(wave_max(r.wflo));
+  r.wfhi = __builtin_amdgcn_readfirstlane(wave_min(r.wfhi));
+  return r;
+}
+
 // ---- dK, dV: key tiles of 128 (plan items of the bounds swapped: segment, key tile), 32 keys per wave. MODE bit 0:
 // compute dV, bit 1: dK.
 template <int D, int MODE>
@@ -368,47 +417,12 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::template occ_k<MODE>()) 
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 31, half = lane >> 5;
 
-  // this lane's key and the query rows that see it: j - right <= i + delta <= j + left, or both in one span
+  // this lane's key and the query rows that see it
   const int key = ktile * keys_per_tile + wave * 32 + col;
   const bool valid = key < lk;
-  int rlo = 0, rhi = 0, srl = 0, srh = 0;
-  int wlo = INT32_MAX, whi = INT32_MIN, wflo = INT32_MIN, wfhi = INT32_MAX;
-  if (valid) {
-    int a = p.right < 0 ? 0 : max(0, key - p.right - delta);
-    int b = p.left < 0 ? lq : (int)min((int64_t)lq, (int64_t)key + p.left - delta + 1);
-    if (b < a) b = a;
-    rlo = a;
-    rhi = b;
-    wflo = a;
-    wfhi = b;
-    if (a < b) {
-      wlo = a;
-      whi = b;
-    }
-    const int kq = key - delta;  // the key's position in query rows
-    if (p.n_spans > 0 && kq >= 0 && kq < lq) {
-      const int row = qa + kq;
-      int l0 = 0, l1 = p.n_spans;
-      while (l1 - l0 > 1) {
-        const int mid = (l0 + l1) >> 1;
-        if (p.spans[2 * mid] <= row) l0 = mid; else l1 = mid;
-      }
-      const int s0 = p.spans[2 * l0], s1 = p.spans[2 * l0 + 1];
-      if (s0 <= row && row < s1) {
-        const int x = max(0, s0 - qa), y = min(lq, s1 - qa);
-        if (x < y) {
-          srl = x;
-          srh = y;
-          wlo = min(wlo, x);
-          whi = max(whi, y);
-        }
-      }
-    }
-  }
-  wlo = __builtin_amdgcn_readfirstlane(wave_min(wlo));
-  whi = __builtin_amdgcn_readfirstlane(wave_max(whi));
-  wflo = __builtin_amdgcn_readfirstlane(wave_max(wflo));
-  wfhi = __builtin_amdgcn_readfirstlane(wave_min(wfhi));
+  const KeyRows seen = key_rows_seen(p, key, valid, qa, lq, delta);
+  const int rlo = seen.lo, rhi = seen.hi, srl = seen.sl, srh = seen.sh;
+  const int wlo = seen.wlo, whi = seen.whi, wflo = seen.wflo, wfhi = seen.wfhi;
   if (lane == 0) {
     red[0][wave] = wlo;
     red[1][wave] = whi;
@@ -690,47 +704,12 @@ __global__ __launch_bounds__(64 * 2 * kBwdWaves, 2) void bwd_dkdv2_kernel(BwdPar
   const int kw = wave & (KW - 1), rs = wave / KW;
   const int col = lane & 31, half = lane >> 5;
 
-  // this lane's key and the query rows that see it (as bwd_dkdv_kernel)
+  // this lane's key and the query rows that see it
   const int key = ktile * keys_per_tile + kw * 32 + col;
   const bool valid = key < lk;
-  int rlo = 0, rhi = 0, srl = 0, srh = 0;
-  int wlo = INT32_MAX, whi = INT32_MIN, wflo = INT32_MIN, wfhi = INT32_MAX;
-  if (valid) {
-    int a = p.right < 0 ? 0 : max(0, key - p.right - delta);
-    int b = p.left < 0 ? lq : (int)min((int64_t)lq, (int64_t)key + p.left - delta + 1);
-    if (b < a) b = a;
-    rlo = a;
-    rhi = b;
-    wflo = a;
-    wfhi = b;
-    if (a < b) {
-      wlo = a;
-      whi = b;
-    }
-    const int kq = key - delta;
-    if (p.n_spans > 0 && kq >= 0 && kq < lq) {
-      const int row = qa + kq;
-      int l0 = 0, l1 = p.n_spans;
-      while (l1 - l0 > 1) {
-        const int mid = (l0 + l1) >> 1;
-        if (p.spans[2 * mid] <= row) l0 = mid; else l1 = mid;
-      }
-      const int s0 = p.spans[2 * l0], s1 = p.spans[2 * l0 + 1];
-      if (s0 <= row && row < s1) {
-        const int x = max(0, s0 - qa), y = min(lq, s1 - qa);
-        if (x < y) {
-          srl = x;
-          srh = y;
-          wlo = min(wlo, x);
-          whi = max(whi, y);
-        }
-      }
-    }
-  }
-  wlo = __builtin_amdgcn_readfirstlane(wave_min(wlo));
-  whi = __builtin_amdgcn_readfirstlane(wave_max(whi));
-  wflo = __builtin_amdgcn_readfirstlane(wave_max(wflo));
-  wfhi = __builtin_amdgcn_readfirstlane(wave_min(wfhi));
+  const KeyRows seen = key_rows_seen(p, key, valid, qa, lq, delta);
+  const int rlo = seen.lo, rhi = seen.hi, srl = seen.sl, srh = seen.sh;
+  const int wlo = seen.wlo, whi = seen.whi, wflo = seen.wflo, wfhi = seen.wfhi;
   if (lane == 0 && rs == 0) {  // group 1 holds the same keys
     red[0][kw] = wlo;
     red[1][kw] = whi;
