@@ -4,7 +4,9 @@
 // families/gemma/sliding_attention.py:50-61, families/gemma/global_attention.py:107-118): with t = scale * q.k over a
 // query row's visible keys, P = exp(t - lse) (the forward's log-sum-exp), D = rowsum(dO * O),
 //   dV = P^T dO,  dP = dO V^T,  dS = P * (dP - D),  dQ = scale * dS K,  dK = scale * dS^T Q.
-// P and dS enter the MFMAs as bf16 (as P does in the forward), every product accumulates in fp32.
+// P and dS enter the MFMAs as bf16 (as P does in the forward), every product accumulates in fp32. The rows'
+// statistics hold -D (negated once where D is formed): the dK / dV kernels start their dP accumulators from it, so
+// dP - D comes out of the MFMAs and a step's softmax saves a subtraction per element.
 //
 // Two kernels after the planner (plan_kernel of attn_fwd.hip: both work lists in one launch; at head sizes 64 and 128
 // the longest key tiles split over their query steps, their parts' fp32 dK / dV summed by bwd_merge_kernel):
@@ -57,7 +59,7 @@ template <int D> struct BwdCfg {
 // Row (within a 32-row step) of result register j of a lane in half `half` (row operands fed in key_row order).
 __device__ __forceinline__ int result_row(int j, int half) { return (j >> 3) * 16 + half * 8 + (j & 7); }
 
-// ---- stats: L = D / 8 lanes per (row, head) vector, 8 elements per lane
+// ---- stats: L = D / 8 lanes per (row, head) vector, 8 elements per lane; the log2 LSE and -D of each
 template <int D>
 __global__ __launch_bounds__(256) void bwd_stats_kernel(BwdParams p) {
   constexpr int L = D / 8, VPW = 64 / L;
@@ -82,7 +84,7 @@ __global__ __launch_bounds__(256) void bwd_stats_kernel(BwdParams p) {
     if (ok && l == 0) {
       const float lse = p.lse[(int64_t)head * p.total_q + row];
       p.stats[((int64_t)head * 2) * p.total_q + row] = lse == -INFINITY ? INFINITY : lse * kLog2e;
-      p.stats[((int64_t)head * 2 + 1) * p.total_q + row] = s;
+      p.stats[((int64_t)head * 2 + 1) * p.total_q + row] = -s;
     }
   }
 }
@@ -163,8 +165,8 @@ __global__ __launch_bounds__(64 * bwd_q_waves(D), BwdCfg<D>::BLOCKS_Q) void bwd_
     red[1][wave] = whi;
   }
   // Q and dO as B operands (lane: its vector, elements dc*16 + half*8 .. +8); the row's log2 LSE and
-  // D = rowsum(dO * O) (the two half-waves hold the two halves of the row), also written for the dK / dV kernel,
-  // which runs after this one (every (row, head) vector is in exactly one query tile)
+  // D = rowsum(dO * O) (the two half-waves hold the two halves of the row), also written (LSE and -D) for the dK / dV
+  // kernel, which runs after this one (every (row, head) vector is in exactly one query tile)
   bf16x8 qop[DC], dop[DC];
   float lse2 = INFINITY, dsum = 0.f;
   {
@@ -191,7 +193,7 @@ __global__ __launch_bounds__(64 * bwd_q_waves(D), BwdCfg<D>::BLOCKS_Q) void bwd_
       lse2 = lse == -INFINITY ? INFINITY : lse * kLog2e;
       if (half == 0) {
         p.stats[((int64_t)head * 2) * p.total_q + qa + pos] = lse2;
-        p.stats[((int64_t)head * 2 + 1) * p.total_q + qa + pos] = dsum;
+        p.stats[((int64_t)head * 2 + 1) * p.total_q + qa + pos] = -dsum;
       }
     }
   }
@@ -545,7 +547,16 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::template occ_k<MODE>()) 
     const int r0 = r_cur;
     r_cur = r_cur == r_first ? r_last : r_cur - BQ;
     if (r0 < whi && r0 + BQ > wlo) {
+      // dP starts from -D of this lane's result rows (half*8 .. and 16 + half*8 ..): the MFMAs leave dP - D
       f32x16 st = f32x16{}, dpt = f32x16{};
+      if constexpr (DK) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const f32x4 nd = *(const KA_LDS f32x4*)(tst + BQ + (u >> 1) * 16 + half * 8 + (u & 1) * 4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) dpt[4 * u + e] = nd[e];
+        }
+      }
 #pragma unroll
       for (int dc = 0; dc < DC; ++dc) {
         const bf16x8 a = *(const KA_LDS bf16x8*)(tqk + q_read[dc & 1] + (dc >> 1) * 1024);
@@ -555,14 +566,10 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::template occ_k<MODE>()) 
           dpt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, vop[dc], dpt, 0, 0, 0);
         }
       }
-      // the step rows' log2 LSE and D for this lane's result registers (rows half*8 .. and 16 + half*8 ..)
-      f32x4 ls[4], ds[4];
+      // the step rows' log2 LSE for this lane's result registers
+      f32x4 ls[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int r = (u >> 1) * 16 + half * 8 + (u & 1) * 4;
-        ls[u] = *(const KA_LDS f32x4*)(tst + r);
-        ds[u] = *(const KA_LDS f32x4*)(tst + BQ + r);
-      }
+      for (int u = 0; u < 4; ++u) ls[u] = *(const KA_LDS f32x4*)(tst + (u >> 1) * 16 + half * 8 + (u & 1) * 4);
       // exponents of P; on a step some lane's window or span cuts, -inf for the rows that do not see the lane's key
       // (one uniform branch around the masking)
       float x[2 * KC * 4];
@@ -585,7 +592,7 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::template occ_k<MODE>()) 
           const int jj = kc * 8 + t;
           const float pr = __builtin_amdgcn_exp2f(x[jj]);
           if constexpr (DV) pb[kc][t] = (__bf16)pr;
-          if constexpr (DK) dsb[kc][t] = (__bf16)(pr * (dpt[jj] - ds[jj >> 2][jj & 3]));
+          if constexpr (DK) dsb[kc][t] = (__bf16)(pr * dpt[jj]);
         }
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc) {
@@ -840,7 +847,14 @@ __global__ __launch_bounds__(64 * 2 * kBwdWaves, 2) void bwd_dkdv2_kernel(BwdPar
       int qr0 = q_read[0], qr1 = q_read[1], kr0 = k_read[0], kr1 = k_read[1], tr0 = t_read[0], tr1 = t_read[1];
       asm volatile("" : "+v"(qr0), "+v"(qr1), "+v"(kr0), "+v"(kr1), "+v"(tr0), "+v"(tr1));
       const int qr[2] = {qr0, qr1}, kr[2] = {kr0, kr1}, tr[2] = {tr0, tr1};
-      f32x16 st = f32x16{}, dpt = f32x16{};
+      // dP starts from -D of this lane's result rows: the MFMAs leave dP - D
+      f32x16 st = f32x16{}, dpt;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const f32x4 nd = *(const KA_LDS f32x4*)(tst + BQ + 2 * BQ * rs + (u >> 1) * 16 + half * 8 + (u & 1) * 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dpt[4 * u + e] = nd[e];
+      }
 #pragma unroll
       for (int dc = 0; dc < DC; ++dc) {
         const int at = (dc >> 1) * 1024;
@@ -851,13 +865,10 @@ __global__ __launch_bounds__(64 * 2 * kBwdWaves, 2) void bwd_dkdv2_kernel(BwdPar
         const bf16x8 vb = *(const KA_LDS bf16x8*)(vt + kr[dc & 1] + at);
         dpt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, vb, dpt, 0, 0, 0);
       }
-      f32x4 ls[4], ds[4];
+      f32x4 ls[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int r = 2 * BQ * rs + (u >> 1) * 16 + half * 8 + (u & 1) * 4;
-        ls[u] = *(const KA_LDS f32x4*)(tst + r);
-        ds[u] = *(const KA_LDS f32x4*)(tst + BQ + r);
-      }
+      for (int u = 0; u < 4; ++u)
+        ls[u] = *(const KA_LDS f32x4*)(tst + 2 * BQ * rs + (u >> 1) * 16 + half * 8 + (u & 1) * 4);
       float x[2 * KC * 4];
 #pragma unroll
       for (int jj = 0; jj < 2 * KC * 4; ++jj) x[jj] = __builtin_fmaf(st[jj], c, -ls[jj >> 2][jj & 3]);
@@ -878,7 +889,7 @@ __global__ __launch_bounds__(64 * 2 * kBwdWaves, 2) void bwd_dkdv2_kernel(BwdPar
           const int jj = kc * 8 + t;
           const float pr = __builtin_amdgcn_exp2f(x[jj]);
           pb[kc][t] = (__bf16)pr;
-          dsb[kc][t] = (__bf16)(pr * (dpt[jj] - ds[jj >> 2][jj & 3]));
+          dsb[kc][t] = (__bf16)(pr * dpt[jj]);
         }
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc) {

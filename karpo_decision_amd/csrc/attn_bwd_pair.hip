@@ -102,7 +102,7 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void bwd_dq_pair_kernel(BwdPara
   }
   // this wave's half of Q and dO as B operands (elements dh*DH + c*16 + half*8 .. +8), the row's log2 LSE and D
   bf16x8 qop[QC], dop[QC];
-  float lse2 = INFINITY, dsum = 0.f;
+  float lse2 = INFINITY, ndsum = 0.f;  // the row's log2 LSE and -D (the statistics pass's)
   {
     const uint16_t* qp = p.q + (int64_t)(qa + pos) * p.sq_t + (int64_t)head * p.sq_h + dh * DH + half * 8;
     const uint16_t* op = p.dout + (int64_t)(qa + pos) * p.sdo_t + (int64_t)head * p.sdo_h + dh * DH + half * 8;
@@ -118,7 +118,7 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void bwd_dq_pair_kernel(BwdPara
     }
     if (valid) {
       lse2 = p.stats[((int64_t)head * 2) * p.total_q + qa + pos];
-      dsum = p.stats[((int64_t)head * 2 + 1) * p.total_q + qa + pos];
+      ndsum = p.stats[((int64_t)head * 2 + 1) * p.total_q + qa + pos];
     }
   }
   __syncthreads();
@@ -219,7 +219,7 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void bwd_dq_pair_kernel(BwdPara
       for (int kc = 0; kc < KC; ++kc)
 #pragma unroll
         for (int t = 0; t < 8; ++t)
-          dsb[kc][t] = (__bf16)(__builtin_amdgcn_exp2f(x[kc][t]) * (dpt[kc * 8 + t] - dsum));
+          dsb[kc][t] = (__bf16)(__builtin_amdgcn_exp2f(x[kc][t]) * (dpt[kc * 8 + t] + ndsum));
       // dQ^T (this wave's half of D) += K^T dS^T, K read transposed
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc)
@@ -468,7 +468,7 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void bwd_dkdv_pair_kernel(BwdPa
       for (int t = 0; t < 8; ++t) {
         const float pr = __builtin_amdgcn_exp2f(x[t]);
         pm[t] = (__bf16)pr;
-        dm[t] = (__bf16)(pr * (pv[t] - (t < 4 ? d0[t] : d1[t - 4])));
+        dm[t] = (__bf16)(pr * (pv[t] + (t < 4 ? d0[t] : d1[t - 4])));  // d0, d1: -D
       }
       pmine[lane] = pm;
       pmine[64 + lane] = dm;
