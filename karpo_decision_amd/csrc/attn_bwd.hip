@@ -842,11 +842,7 @@ __global__ __launch_bounds__(64 * 2 * kBwdWaves, 2) void bwd_dkdv2_kernel(BwdPar
     const int r0 = r_cur;
     r_cur = next_row(next_row(r_cur));
     if (i < my_steps && r0 < whi && r0 + BQ > wlo) {
-      // the lanes' read offsets, opaque per step: their sums with the reads' constants stay in the instructions'
-      // offset fields instead of 16 registers held across the loop
-      int qr0 = q_read[0], qr1 = q_read[1], kr0 = k_read[0], kr1 = k_read[1], tr0 = t_read[0], tr1 = t_read[1];
-      asm volatile("" : "+v"(qr0), "+v"(qr1), "+v"(kr0), "+v"(kr1), "+v"(tr0), "+v"(tr1));
-      const int qr[2] = {qr0, qr1}, kr[2] = {kr0, kr1}, tr[2] = {tr0, tr1};
+      const int(&qr)[2] = q_read, (&kr)[2] = k_read, (&tr)[2] = t_read;
       // dP starts from -D of this lane's result rows: the MFMAs leave dP - D
       f32x16 st = f32x16{}, dpt;
 #pragma unroll
