@@ -11,7 +11,7 @@
 // Two kernels after the planner (plan_kernel of attn_fwd.hip: both work lists in one launch; at head sizes 64 and 128
 // the longest key tiles split over their query steps, their parts' fp32 dK / dV summed by bwd_merge_kernel):
 //   * bwd_dq_kernel (query-stationary, the forward's tiles): per (head, query row) first the log2-domain LSE (+inf
-//     for a row that sees no key, so its P are 0) and D = rowsum(dO * O), written for the dK / dV kernel (every
+//     for a row that sees no key, so its P are 0) and -D = -rowsum(dO * O), written for the dK / dV kernel (every
 //     vector is in exactly one query tile); then Q and dO of 32 query vectors per wave as MFMA B operands
 //     in registers, K and V streamed through LDS; S^T = K Q^T and dP^T = V dO^T with K and V read as row operands,
 //     dQ^T += K^T dS^T with K read transposed from the same tile (the S layout of mfma_common.h serves both reads);
@@ -398,7 +398,7 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::template occ_k<MODE>()) 
   __shared__ __attribute__((aligned(1024))) char qk1[TILE];
   __shared__ __attribute__((aligned(1024))) char ok0[TILE];  // dO (S layout: rows for dP, transposed for dV; dV alone: transposed-read layout)
   __shared__ __attribute__((aligned(1024))) char ok1[TILE];
-  __shared__ __attribute__((aligned(256))) float sts0[2 * BQ];  // log2 LSE, then D, of the step's rows
+  __shared__ __attribute__((aligned(256))) float sts0[2 * BQ];  // log2 LSE, then -D, of the step's rows
   __shared__ __attribute__((aligned(256))) float sts1[2 * BQ];
   __shared__ int red[2][W];
 
@@ -510,7 +510,7 @@ __global__ __launch_bounds__(64 * kBwdWaves, BwdCfg<D>::template occ_k<MODE>()) 
         dma_16b(qs, rows * (int)p.sq_t * 2, tqk + at, qk_off[r]);
         dma_16b(os, rows * (int)p.sdo_t * 2, tok + at, ok_off[r]);
       }
-    if (wave == W - 1) {  // 32 log2 LSE (lanes 0-31) then 32 D (lanes 32-63), 4 B per lane; zeros past the stats
+    if (wave == W - 1) {  // 32 log2 LSE (lanes 0-31) then 32 -D (lanes 32-63), 4 B per lane; zeros past the stats
       const __amdgpu_buffer_rsrc_t rs =
           __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, (int)(p.total_q + rows) * 4, kBufferFlags);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (KA_LDS void*)tst, 4,
@@ -689,7 +689,7 @@ __global__ __launch_bounds__(64 * 2 * kBwdWaves, 2) void bwd_dkdv2_kernel(BwdPar
   __shared__ __attribute__((aligned(1024))) char qk1[2][TILE];
   __shared__ __attribute__((aligned(1024))) char ok0[2][TILE];   // per group: dO (S layout)
   __shared__ __attribute__((aligned(1024))) char ok1[2][TILE];
-  __shared__ __attribute__((aligned(256))) float sts0[2][2 * BQ];  // per group: log2 LSE, then D, of the step's rows
+  __shared__ __attribute__((aligned(256))) float sts0[2][2 * BQ];  // per group: log2 LSE, then -D, of the step's rows
   __shared__ __attribute__((aligned(256))) float sts1[2][2 * BQ];
   __shared__ int red[2][KW];
 
@@ -805,7 +805,7 @@ __global__ __launch_bounds__(64 * 2 * kBwdWaves, 2) void bwd_dkdv2_kernel(BwdPar
       dma_16b(qs, rows * (int)p.sq_t * 2, tqk + at, qk_off[r]);
       dma_16b(os, rows * (int)p.sdo_t * 2, tok + at, ok_off[r]);
     }
-    if (kw == KW - 1) {  // 32 log2 LSE (lanes 0-31) then 32 D (lanes 32-63), 4 B per lane; zeros past the stats
+    if (kw == KW - 1) {  // 32 log2 LSE (lanes 0-31) then 32 -D (lanes 32-63), 4 B per lane; zeros past the stats
       const __amdgpu_buffer_rsrc_t rsrc =
           __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, (int)(p.total_q + rows) * 4, kBufferFlags);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (KA_LDS void*)(tst + 2 * BQ * rs), 4,

@@ -276,7 +276,7 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void bwd_dkdv_pair_kernel(BwdPa
   __shared__ __attribute__((aligned(1024))) char q1_s[TILE];  // Q of odd steps
   __shared__ __attribute__((aligned(1024))) char o0_s[TILE];  // dO of even steps (S layout: rows for dP, transposed for dV)
   __shared__ __attribute__((aligned(1024))) char o1_s[TILE];  // dO of odd steps
-  __shared__ __attribute__((aligned(256))) float st_s[2][2 * BQ];  // log2 LSE, then D, of a step's rows (by parity)
+  __shared__ __attribute__((aligned(256))) float st_s[2][2 * BQ];  // log2 LSE, then -D, of a step's rows (by parity)
   __shared__ __attribute__((aligned(16))) f32x4 xch[W][4 * 64];    // partial S and dP of the partner's row block
   __shared__ __attribute__((aligned(16))) bf16x8 pxch[W][2 * 64];  // P and dS of the wave's row block
   __shared__ int red[2][W];
@@ -359,7 +359,7 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void bwd_dkdv_pair_kernel(BwdPa
       dma_16b(c_q, rows * (int)p.sq_t * 2, dq_ + at, s_block(q_off, r));
       dma_16b(c_o, rows * (int)p.sdo_t * 2, do_ + at, s_block(o_off, r));
     }
-    if (wave == W - 1) {  // 32 log2 LSE (lanes 0-31) then 32 D (lanes 32-63), 4 B per lane; zeros past the stats
+    if (wave == W - 1) {  // 32 log2 LSE (lanes 0-31) then 32 -D (lanes 32-63), 4 B per lane; zeros past the stats
       const __amdgpu_buffer_rsrc_t rs =
           __builtin_amdgcn_make_buffer_rsrc((void*)c_st, (short)0, (int)(p.total_q + rows) * 4, kBufferFlags);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (KA_LDS void*)dst, 4, st_off, 0, 0, 0);

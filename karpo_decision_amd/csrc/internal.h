@@ -47,7 +47,7 @@ struct Params {
 };
 
 // The backward kernels' arguments (karpo_attn_bwd): the forward's tensors and bounds, the output gradient and the
-// gradients to write; stats holds (log2-domain LSE, rowsum(dO * O)) per (head, query row).
+// gradients to write; stats holds (log2-domain LSE, -rowsum(dO * O)) per (head, query row).
 struct BwdParams {
   const uint16_t* __restrict__ q;
   const uint16_t* __restrict__ k;
@@ -58,7 +58,7 @@ struct BwdParams {
   uint16_t* __restrict__ dq;
   uint16_t* __restrict__ dk;
   uint16_t* __restrict__ dv;
-  float* __restrict__ stats;  // [heads][2][total_q]: each row's log2-domain LSE, then rowsum(dout * o)
+  float* __restrict__ stats;  // [heads][2][total_q]: each row's log2-domain LSE, then -rowsum(dout * o)
   int64_t sq_t, sq_h, sk_t, sk_h, sv_t, sv_h, so_t, so_h, sdo_t, sdo_h, sdq_t, sdq_h, sdk_t, sdk_h, sdv_t, sdv_h;
   const int32_t* __restrict__ q_cu;
   const int32_t* __restrict__ k_cu;
