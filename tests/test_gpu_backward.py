@@ -6,7 +6,8 @@ the error of the oracle's own bf16 run plus 2e-3 (the reference's criterion for 
 tests/gpu/test_packed_gemma.py:173-184). The log-sum-exp within 1e-2 absolute of the oracle's float64 value (P sums
 are bf16-rounded in the kernel), -inf exactly for rows that see no key. Layouts: causal GQA with an empty and a
 one-row sequence, branches (Lk > Lq), more queries than keys, sliding and two-sided windows, image spans,
-bidirectional packs, a group size that does not divide a tile, negative scale; bitwise-equal repeated calls.
+bidirectional packs, a group size that does not divide a tile, negative and zero scales (at zero the oracle's dq and
+dk are exact zeros, and so must the kernels' be); bitwise-equal repeated calls.
 """
 
 from __future__ import annotations
@@ -68,6 +69,8 @@ LAYOUTS = [
     ([700, 333], [700, 333], 16, 2, 128, -1, 0, [], None),               # group 8: steps cross head boundaries
     ([500, 47], [500, 47], 16, 4, 128, 100, 0, [], None),                # group 4 under a window
     ([100], [130], 4, 2, 128, 31, 0, [], -0.09),                         # negative scale, window, branch
+    ([90, 33], [90, 33], 4, 2, 128, -1, 0, [], 0.0),                     # zero scale: P uniform, dQ = dK = 0
+    ([70, 51], [90, 51], 4, 2, 256, 40, 0, [], 0.0),                     # zero scale at 256 under a window
     ([96, 64], [96, 64], 4, 2, 256, -1, 0, [(1, 8, 40)], None),
     ([300, 1, 0, 130], [300, 1, 0, 130], 8, 1, 512, -1, 0, [], None),   # head size 512: wave pairs
     ([64, 100], [200, 100], 8, 2, 512, -1, 0, [(1, 10, 40)], None),      # branches and a span at 512
